@@ -1,0 +1,195 @@
+/*
+ * t0hip.h — C ABI of the MI355X-native t0 quantized-inference engine.
+ *
+ * This is the boundary a Rust `t0-hip` crate (or any FFI) binds: plain C
+ * types, host or device pointers plus sizes, int status codes, no exceptions
+ * and no aborts across it.  Each entry point names the reference interface
+ * it replaces (paths relative to idle-intelligence/t0-web):
+ *
+ *   t0h_ctx   ≡ t0_fast::Engine   (crates/t0-fast/src/engine.rs:18-44)
+ *   t0h_model ≡ t0_fast::GpuModel (crates/t0-fast/src/model.rs:170-187)
+ *
+ * Threading: calls on one t0h_model are serialized by the caller (the
+ * reference's "forward calls are sequential" contract, pool.rs:9-16); distinct
+ * models may share one t0h_ctx and run concurrently, each on its own HIP
+ * stream with its own workspace.
+ *
+ * Memory: host-pointer entry points copy in and out (outputs are written to
+ * caller-owned buffers of the stated length).  Entry points suffixed `_dev`
+ * take device pointers and run on the model's stream without host copies.
+ */
+#ifndef T0HIP_H
+#define T0HIP_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define T0H_ABI_VERSION 1
+#define T0H_MAX_QUANTILES 64
+#define T0H_MAX_HORIZON 1024 /* crates/t0-core/src/model.rs:26 MAX_HORIZON */
+#define T0H_MAX_PATCHES 256  /* time-attention window per forward, in patches */
+
+/* Status codes.  Each maps one reference failure (anyhow error or panic). */
+enum t0h_status {
+  T0H_OK = 0,
+  T0H_ERR_INVALID_ARG = -1,      /* bad pointer/length; assert!s in lib.rs:195 */
+  T0H_ERR_GGUF_MAGIC = -2,       /* gguf.rs:350-352 "not a GGUF file (bad magic)" */
+  T0H_ERR_GGUF_VERSION = -3,     /* gguf.rs:353-356 unsupported GGUF version */
+  T0H_ERR_GGUF_TENSOR_TYPE = -4, /* gguf.rs:41-49 unsupported ggml tensor type id */
+  T0H_ERR_GGUF_META_TYPE = -5,   /* gguf.rs:281-283, 290 unsupported metadata value type */
+  T0H_ERR_GGUF_BOUNDS = -6,      /* gguf.rs:397-400 tensor out of blob; truncated file */
+  T0H_ERR_MISSING_TENSOR = -7,   /* weights.rs:268-270, t0-fast model.rs:255-257 */
+  T0H_ERR_METADATA = -8,         /* weights.rs:70-97 missing/wrong-typed t0.* key; bad utf-8 */
+  T0H_ERR_HORIZON = -9,          /* lib.rs:58-62 padded horizon > MAX_HORIZON */
+  T0H_ERR_FUTURE_ROWS = -10,     /* scaler.rs:52-54 FUTURE covariate rows */
+  T0H_ERR_NO_DEVICE = -11,       /* engine.rs:64-81 no GPU adapter */
+  T0H_ERR_HIP = -12,             /* a HIP runtime call failed */
+  T0H_ERR_SHAPE = -13,           /* tensor shape inconsistent with the config */
+  T0H_ERR_UNSUPPORTED = -14,     /* outside this engine's documented limits */
+  T0H_ERR_OOM = -15,             /* host or device allocation failed */
+};
+
+/* ggml tensor type ids (gguf.rs:31-49) */
+enum t0h_qtype { T0H_F32 = 0, T0H_F16 = 1, T0H_Q4_0 = 2, T0H_Q8_0 = 8 };
+
+/* MaskType (data.rs:6-13) and VariateType (data.rs:15-20) */
+enum { T0H_MASK_VALID = 0, T0H_MASK_PAD = 1, T0H_MASK_MISSING = 2, T0H_MASK_CENSORED = 3, T0H_MASK_WITHHELD = 4 };
+enum { T0H_VT_TARGET = 0, T0H_VT_HISTORICAL = 1, T0H_VT_FUTURE = 2 };
+
+/* ≡ T0Config (crates/t0-core/src/config.rs:6-22) */
+typedef struct {
+  uint32_t embed_dim, num_layers, num_heads, mlp_hidden_dim, patch_size;
+  int64_t group_every_n;
+  float dropout;
+  uint32_t n_quantiles;
+  float quantile_levels[T0H_MAX_QUANTILES];
+  int32_t scaler_use_arcsinh;
+  float scaler_eps;
+  int32_t scaler_variance_offset; /* 1: "variance_offset", 0: "std_clamp" (scaler.rs:28-34) */
+} t0h_config;
+
+/* ≡ t0_core::data::TimeSeries (data.rs:24-33); all arrays row-major [v, t]. */
+typedef struct {
+  size_t v, t;
+  const float* variates;
+  const int8_t* mask;
+  const int64_t* group_ids;
+  const int64_t* variate_type;
+} t0h_series;
+
+typedef struct t0h_ctx t0h_ctx;
+typedef struct t0h_model t0h_model;
+
+/* ---- errors / version -------------------------------------------------- */
+/* Message of the last failing call on this thread (≡ anyhow::Error's text). */
+const char* t0h_last_error(void);
+int t0h_abi_version(void);
+
+/* ---- engine ------------------------------------------------------------ */
+/* ≡ Engine::new_async (engine.rs:62-106).  T0H_ERR_NO_DEVICE when no GPU. */
+int t0h_ctx_create(int device, t0h_ctx** out);
+void t0h_ctx_destroy(t0h_ctx* ctx);
+
+/* ---- model ------------------------------------------------------------- */
+/* Parse and validate a GGUF (read_gguf gguf.rs:347-405 + config_from_gguf_metadata
+ * weights.rs:69-112 + the tensor set T0Model::load needs, model.rs:108-147)
+ * without touching a GPU.  cfg may be NULL. */
+int t0h_gguf_inspect(const uint8_t* bytes, size_t len, t0h_config* cfg, size_t* n_tensors);
+
+/* ≡ t0_fast::load_model_from_gguf (lib.rs:42-44 → GpuModel::load_from_gguf_bytes,
+ * model.rs:302-348).  Q8_0/Q4_0 blocks are uploaded verbatim (llama.cpp AoS
+ * layout) and stay resident; F16 matrices stay f16; F32 matrices are held as
+ * f16; vectors (biases, norm scales, type embeddings) are held as f32. */
+int t0h_model_load_gguf(t0h_ctx* ctx, const uint8_t* bytes, size_t len, t0h_model** out);
+void t0h_model_destroy(t0h_model* model);
+int t0h_model_config(const t0h_model* model, t0h_config* out);
+/* ≡ GpuModel::quantizable_gpu_bytes / total_weight_bytes (model.rs:194-225) */
+int t0h_model_weight_bytes(const t0h_model* model, uint64_t* quantizable, uint64_t* total);
+/* The hipStream_t this model's work is issued on. */
+void* t0h_model_stream(const t0h_model* model);
+/* Device workspace currently held (≡ Pool::resident_bytes, pool.rs:64-66) and the
+ * number of device allocations made since load (≡ Pool::alloc_count, pool.rs:51-57). */
+int t0h_model_workspace(const t0h_model* model, uint64_t* resident_bytes, uint64_t* alloc_count);
+
+/* ---- forward ----------------------------------------------------------- */
+/* ≡ model::forward_async (t0-fast model.rs:693-808) ≡ T0Model::forward (t0-core
+ * model.rs:159-244): `series` already padded to whole patches and scaled.
+ * out: [v, p, patch_size, n_quantiles] raw quantile-head output, p = t/patch.
+ * trace_patch_emb / trace_layer0: optional [v, p, embed_dim] taps (model.rs:79-82). */
+int t0h_forward(t0h_model* model, const t0h_series* series, float* out, size_t out_len, float* trace_patch_emb,
+                float* trace_layer0);
+
+/* ---- forecast entry points (outputs [rows, horizon, n_quantiles]) -------- */
+/* ≡ t0_fast::forecast (lib.rs:102-109): v rows of one joint series (group 0). */
+int t0h_forecast(t0h_model* model, const float* context, size_t v, size_t t_ctx, size_t horizon, float* out,
+                 size_t out_len);
+/* ≡ t0_fast::forecast_batch_chunked (lib.rs:118-146): independent univariate
+ * signals, one group id each, chunk_size signals per forward (0 = one forward). */
+int t0h_forecast_batch_chunked(t0h_model* model, const float* contexts, size_t n_signals, size_t t_ctx,
+                               size_t horizon, size_t chunk_size, float* out, size_t out_len);
+/* ≡ t0_fast::forecast_batch_rows_chunked (lib.rs:175-248): ragged contexts
+ * concatenated per `lengths`. */
+int t0h_forecast_batch_rows_chunked(t0h_model* model, const float* contexts, const size_t* lengths, size_t n_signals,
+                                    size_t horizon, size_t chunk_size, float* out, size_t out_len);
+/* Multivariate batch with an explicit group id per row (the 256 series x 3
+ * variates workload).  The reference has no public entry point for this; it is
+ * built from TimeSeries' pub fields the way lib.rs:208-236 builds its rows. */
+int t0h_forecast_grouped(t0h_model* model, const float* contexts, const int64_t* row_group, size_t n_rows,
+                         size_t t_ctx, size_t horizon, float* out, size_t out_len);
+/* Same, device-resident: d_contexts [n_rows, t_ctx] and d_out [n_rows, horizon,
+ * n_q] are device pointers; row_group is a host array.  Work is issued on the
+ * model's stream; the call returns once it is enqueued (synchronize the stream
+ * before reading d_out). */
+int t0h_forecast_grouped_dev(t0h_model* model, const float* d_contexts, const int64_t* row_group, size_t n_rows,
+                             size_t t_ctx, size_t horizon, float* d_out);
+/* Autoregressive loop over t0h_forecast_grouped: after each step every row's
+ * median-level quantile is appended and the window re-cut to the trailing
+ * t_ctx values, weights staying resident.  out: [n_rows, steps*horizon, n_q]. */
+int t0h_forecast_grouped_ar(t0h_model* model, const float* contexts, const int64_t* row_group, size_t n_rows,
+                            size_t t_ctx, size_t horizon, size_t steps, float* out, size_t out_len);
+/* ≡ t0_fast::forecast_rollout (lib.rs:259-341) ≡ t0_core::forecast_rollout
+ * (model.rs:582-665): one univariate series; out [prediction_length, n_query]. */
+int t0h_forecast_rollout(t0h_model* model, const float* context, size_t t_ctx, size_t prediction_length,
+                         const float* query_levels, size_t n_query, float* out, size_t out_len);
+
+/* ---- kernel-level entry points (device pointers, stream = hipStream_t or NULL) ---- */
+/* Bit-exact dequantization ≡ dequantize_for (gguf.rs:213-226) on device. */
+int t0h_dequant(int qtype, const void* d_blocks, size_t n_elements, float* d_out, void* stream);
+/* ≡ t0-fast linear() (model.rs:406-504) / ops::linear (ops.rs:40-42):
+ * d_y[m,n] = sum_k d_x[m,k] * W[n,k] + d_bias[n] (d_bias may be NULL), act 1 = relu.
+ * W is [n, k] in GGUF layout of `wtype` (F16, Q8_0, Q4_0).  f32 in, f32 out. */
+int t0h_gemm_q(int wtype, const void* d_w, const float* d_x, const float* d_bias, float* d_y, size_t m, size_t n,
+               size_t k, int act, void* stream);
+
+/* ---- host codec, export, synthetic model -------------------------------- */
+/* GgmlType::row_bytes (gguf.rs:61-70); 0 for an invalid count. */
+size_t t0h_row_bytes(int qtype, size_t n_elements);
+/* ≡ quantize_for (gguf.rs:192-211), host. */
+int t0h_quantize(int qtype, const float* x, size_t n, uint8_t* out, size_t out_len);
+
+typedef struct {
+  t0h_config config;
+  uint64_t seed;
+  float weight_std;     /* rank-2 matrices ~ N(0, weight_std) */
+  float bias_std;       /* biases ~ N(0, bias_std) */
+  float norm_std;       /* norm scales ~ 1 + N(0, norm_std) */
+  float emb_std;        /* type embeddings ~ N(0, emb_std) */
+  float increment_bias; /* decoder output bias of quantile columns 1..n_q-1 */
+} t0h_synth_spec;
+
+/* Random-init model of the given config, written as GGUF the way
+ * Weights::export_gguf (weights.rs:187-227) writes it: the four big per-layer
+ * matmuls as `quant` (T0H_F16/T0H_Q8_0/T0H_Q4_0), everything else F16; quant =
+ * T0H_F32 writes every tensor as F32.  Call with out = NULL to get *len. */
+int t0h_synth_model_gguf(const t0h_synth_spec* spec, int quant, uint8_t* out, size_t cap, size_t* len);
+/* Re-export a GGUF's tensors with another quantization (≡ export_gguf). */
+int t0h_export_gguf(const uint8_t* bytes, size_t len, int quant, uint8_t* out, size_t cap, size_t* out_len);
+
+#ifdef __cplusplus
+}
+#endif
+#endif /* T0HIP_H */

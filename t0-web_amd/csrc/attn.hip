@@ -1,0 +1,320 @@
+// Attention for gfx950, reading the fused QKV activations in place.
+//
+// Semantics: ops.rs:153-190 (mhsa) with the masks of mask.rs:49-82 derived on
+// the fly from per-patch metadata instead of dense [v,p,p] / [p,v,v] float
+// masks:
+//   time layers  — query patch i of variate row r attends key patch j iff
+//                  (row is FUTURE or j <= i) and g_i >= 0 and g_j == g_i and
+//                  patch j is attendable (mask.rs:49-65);
+//   group layers — at a fixed patch, variate row a attends row b iff
+//                  g_a >= 0 and g_b == g_a (mask.rs:69-82).
+// A query whose every key is blocked gets the reference's result for an
+// all-(-1e9) score row: exp(0) for every key, i.e. uniform weights over all
+// keys of the row (time) or all variate rows (group).
+// Per head: QK-RMSNorm (eps 1e-8) before RoPE (ops.rs:175-181), interleaved
+// xPos RoPE on time layers (ops.rs:132-142; q scaled by the xpos table, k by
+// its reciprocal), scores * 1/sqrt(head_dim), softmax, P*V.
+#include <hip/hip_runtime.h>
+
+#include <string>
+
+#include "kernels.h"
+#include "t0hip_internal.h"
+
+namespace t0h {
+namespace {
+
+typedef _Float16 half8 __attribute__((ext_vector_type(8)));
+typedef _Float16 half4 __attribute__((ext_vector_type(4)));
+typedef float floatx4 __attribute__((ext_vector_type(4)));
+
+constexpr int HD = 64;
+constexpr int LDH = HD + 8;
+constexpr int MAXKT = T0H_MAX_PATCHES / 16;
+
+__host__ __device__ inline int round_up(int x, int m) { return (x + m - 1) / m * m; }
+
+size_t time_attn_lds(int p) {
+  const int P16 = round_up(p, 16), P32 = round_up(p, 32);
+  return (size_t)(P16 + P32) * LDH * 2 + (size_t)HD * (P32 + 8) * 2 + (size_t)P32 * 4 + (size_t)P32;
+}
+
+// One workgroup per (variate row, head); 4 waves; MFMA 16x16x32 f16 for both
+// S^T = K Q^T and O = P V, scores of a 16-query tile kept in registers.
+__global__ __launch_bounds__(256) void k_time_attn(const AttnDesc d) {
+  extern __shared__ __align__(16) _Float16 sm[];
+  const int p = d.p, P16 = round_up(p, 16), P32 = round_up(p, 32), LDV = P32 + 8;
+  _Float16* Qs = sm;
+  _Float16* Ks = Qs + P16 * LDH;
+  _Float16* Vt = Ks + P32 * LDH;
+  int* Gk = reinterpret_cast<int*>(Vt + HD * LDV);
+  uint8_t* Ak = reinterpret_cast<uint8_t*>(Gk + P32);
+
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int r = blockIdx.x / d.heads, h = blockIdx.x % d.heads;
+  const int E = d.E, ld = 3 * E;
+  const size_t row0 = (size_t)r * p;
+
+  for (int i = tid; i < P32; i += 256) {
+    Gk[i] = i < p ? d.grp[row0 + i] : -2;
+    Ak[i] = i < p ? d.att[row0 + i] : 0;
+  }
+  // load q, k (normalized + rotated) and v (transposed) for this head
+  for (int task = tid; task < 3 * P32; task += 256) {
+    const int which = task / P32, i = task % P32;
+    if (which == 0 && i >= P16) continue;
+    if (i >= p) {
+      if (which < 2) {
+        uint4* dst = reinterpret_cast<uint4*>((which ? Ks : Qs) + i * LDH);
+#pragma unroll
+        for (int c = 0; c < 8; ++c) dst[c] = make_uint4(0, 0, 0, 0);
+      } else {
+        for (int dd = 0; dd < HD; ++dd) Vt[dd * LDV + i] = (_Float16)0.0f;
+      }
+      continue;
+    }
+    const uint4* src = reinterpret_cast<const uint4*>(d.qkv + (row0 + i) * ld + (size_t)which * E + h * HD);
+    _Float16 xh[HD];
+#pragma unroll
+    for (int c = 0; c < 8; ++c) {
+      const half8 v = __builtin_bit_cast(half8, src[c]);
+#pragma unroll
+      for (int e = 0; e < 8; ++e) xh[c * 8 + e] = v[e];
+    }
+    if (which == 2) {
+#pragma unroll
+      for (int dd = 0; dd < HD; ++dd) Vt[dd * LDV + i] = xh[dd];
+      continue;
+    }
+    float x[HD];
+    float ss = 0.0f;
+#pragma unroll
+    for (int dd = 0; dd < HD; ++dd) {
+      x[dd] = (float)xh[dd];
+      ss += x[dd] * x[dd];
+    }
+    const float denom = sqrtf(ss / (float)HD + 1e-8f);
+    const float* nrm = which ? d.k_norm : d.q_norm;
+#pragma unroll
+    for (int dd = 0; dd < HD; ++dd) x[dd] = (x[dd] / denom) * nrm[dd];
+    const float* ct = d.rope_cos + (size_t)i * HD;
+    const float* st = d.rope_sin + (size_t)i * HD;
+    const float* xt = d.rope_scale + (size_t)i * HD;
+    uint4* dst = reinterpret_cast<uint4*>((which ? Ks : Qs) + i * LDH);
+#pragma unroll
+    for (int c = 0; c < 8; ++c) {
+      half8 o;
+#pragma unroll
+      for (int e = 0; e < 8; ++e) {
+        const int dd = c * 8 + e;
+        const float sv = which ? 1.0f / xt[dd] : xt[dd];
+        const float rot = (dd & 1) ? x[dd - 1] : -x[dd + 1];
+        o[e] = (_Float16)(((x[dd] * ct[dd]) * sv) + ((rot * st[dd]) * sv));
+      }
+      dst[c] = __builtin_bit_cast(uint4, o);
+    }
+  }
+  __syncthreads();
+
+  const bool fut = d.fut[r] != 0;
+  const int nqt = P16 / 16, all_kt = P32 / 16;
+  for (int qt = wave; qt < nqt; qt += 4) {
+    const int q = qt * 16 + (lane & 15);
+    const int gq = q < p ? Gk[q] : -1;
+    const bool need_all = fut || __ballot(q < p && gq < 0) != 0;
+    const int nkt = need_all ? all_kt : min(all_kt, (qt + 2) & ~1);
+    const _Float16* qrow = Qs + (qt * 16 + (lane & 15)) * LDH + (lane >> 4) * 8;
+    const half8 bq0 = *reinterpret_cast<const half8*>(qrow);
+    const half8 bq1 = *reinterpret_cast<const half8*>(qrow + 32);
+
+    float sc[MAXKT][4];
+    float mx = -INFINITY;
+#pragma unroll
+    for (int kt = 0; kt < MAXKT; ++kt) {
+      if (kt < nkt) {
+        const _Float16* krow = Ks + (kt * 16 + (lane & 15)) * LDH + (lane >> 4) * 8;
+        floatx4 s = {0.f, 0.f, 0.f, 0.f};
+        s = __builtin_amdgcn_mfma_f32_16x16x32_f16(*reinterpret_cast<const half8*>(krow), bq0, s, 0, 0, 0);
+        s = __builtin_amdgcn_mfma_f32_16x16x32_f16(*reinterpret_cast<const half8*>(krow + 32), bq1, s, 0, 0, 0);
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          const int key = kt * 16 + (lane >> 4) * 4 + e;
+          const bool ok = key < p && gq >= 0 && Gk[key] == gq && Ak[key] && (fut || key <= q);
+          sc[kt][e] = ok ? s[e] * 0.125f : -INFINITY;
+          mx = fmaxf(mx, sc[kt][e]);
+        }
+      }
+    }
+    mx = fmaxf(mx, __shfl_xor(mx, 16));
+    mx = fmaxf(mx, __shfl_xor(mx, 32));
+    const bool uniform = mx == -INFINITY;
+    float sum = 0.0f;
+#pragma unroll
+    for (int kt = 0; kt < MAXKT; ++kt) {
+      if (kt < nkt) {
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          const int key = kt * 16 + (lane >> 4) * 4 + e;
+          const float ev = uniform ? (key < p ? 1.0f : 0.0f) : __expf(sc[kt][e] - mx);
+          sc[kt][e] = ev;
+          sum += ev;
+        }
+      }
+    }
+    sum += __shfl_xor(sum, 16);
+    sum += __shfl_xor(sum, 32);
+    const float inv = 1.0f / sum;
+
+    floatx4 o[4];
+#pragma unroll
+    for (int dt = 0; dt < 4; ++dt) o[dt] = (floatx4){0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int c = 0; c < MAXKT / 2; ++c) {
+      if (2 * c < nkt) {
+        half8 pa;
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          pa[e] = (_Float16)(sc[2 * c][e] * inv);
+          pa[4 + e] = (_Float16)(sc[2 * c + 1][e] * inv);
+        }
+#pragma unroll
+        for (int dt = 0; dt < 4; ++dt) {
+          const _Float16* vrow = Vt + (dt * 16 + (lane & 15)) * LDV + 32 * c + (lane >> 4) * 4;
+          const half4 lo = *reinterpret_cast<const half4*>(vrow);
+          const half4 hi = *reinterpret_cast<const half4*>(vrow + 16);
+          const half8 bv = {lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
+          o[dt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(pa, bv, o[dt], 0, 0, 0);
+        }
+      }
+    }
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      const int qrow_i = qt * 16 + (lane >> 4) * 4 + e;
+      if (qrow_i < p) {
+        _Float16* dst = d.out + (row0 + qrow_i) * E + h * HD + (lane & 15);
+#pragma unroll
+        for (int dt = 0; dt < 4; ++dt) dst[dt * 16] = (_Float16)o[dt][e];
+      }
+    }
+  }
+}
+
+// Group attention: one thread per (query row, head), keys restricted to the
+// query row's group (segment of a group-sorted permutation); online softmax.
+__global__ __launch_bounds__(256) void k_group_attn(const AttnDesc d) {
+  const int H = d.heads, E = d.E, p = d.p, v = d.v, ld = 3 * E;
+  const long long task = (long long)blockIdx.x * 256 + threadIdx.x;
+  if (task >= (long long)v * p * H) return;
+  const int h = (int)(task % H);
+  const long long m = task / H;
+  const int r = (int)(m / p), pi = (int)(m % p);
+  const int gq = d.grp[m];
+  float o[HD];
+#pragma unroll
+  for (int dd = 0; dd < HD; ++dd) o[dd] = 0.0f;
+
+  auto load = [&](long long row, int which, float (&x)[HD]) {
+    const uint4* src = reinterpret_cast<const uint4*>(d.qkv + row * ld + (size_t)which * E + h * HD);
+#pragma unroll
+    for (int c = 0; c < 8; ++c) {
+      const half8 hv = __builtin_bit_cast(half8, src[c]);
+#pragma unroll
+      for (int e = 0; e < 8; ++e) x[c * 8 + e] = (float)hv[e];
+    }
+  };
+
+  if (gq < 0) {
+    float vv[HD];
+    for (int j = 0; j < v; ++j) {
+      load((long long)j * p + pi, 2, vv);
+#pragma unroll
+      for (int dd = 0; dd < HD; ++dd) o[dd] += vv[dd];
+    }
+    const float inv = 1.0f / (float)v;
+#pragma unroll
+    for (int dd = 0; dd < HD; ++dd) o[dd] *= inv;
+  } else {
+    float qn[HD];
+    load(m, 0, qn);
+    float ss = 0.0f;
+#pragma unroll
+    for (int dd = 0; dd < HD; ++dd) ss += qn[dd] * qn[dd];
+    const float dq = sqrtf(ss / (float)HD + 1e-8f);
+#pragma unroll
+    for (int dd = 0; dd < HD; ++dd) qn[dd] = (qn[dd] / dq) * d.q_norm[dd];
+    float mx = -INFINITY, l = 0.0f;
+    const int b = d.seg_begin[r], n = d.seg_len[r];
+    for (int idx = 0; idx < n; ++idx) {
+      const int j = d.perm[b + idx];
+      const long long mk = (long long)j * p + pi;
+      if (d.grp[mk] != gq) continue;
+      float kx[HD];
+      load(mk, 1, kx);
+      float ks = 0.0f, dot = 0.0f;
+#pragma unroll
+      for (int dd = 0; dd < HD; ++dd) {
+        ks += kx[dd] * kx[dd];
+        dot += qn[dd] * (kx[dd] * d.k_norm[dd]);
+      }
+      const float s = (dot / sqrtf(ks / (float)HD + 1e-8f)) * 0.125f;
+      const float nm = fmaxf(mx, s);
+      const float corr = __expf(mx - nm), pw = __expf(s - nm);
+      l = l * corr + pw;
+      float vx[HD];
+      load(mk, 2, vx);
+#pragma unroll
+      for (int dd = 0; dd < HD; ++dd) o[dd] = o[dd] * corr + pw * vx[dd];
+      mx = nm;
+    }
+    const float inv = l > 0.0f ? 1.0f / l : 0.0f;
+#pragma unroll
+    for (int dd = 0; dd < HD; ++dd) o[dd] *= inv;
+  }
+  uint4* dst = reinterpret_cast<uint4*>(d.out + m * E + h * HD);
+#pragma unroll
+  for (int c = 0; c < 8; ++c) {
+    half8 hv;
+#pragma unroll
+    for (int e = 0; e < 8; ++e) hv[e] = (_Float16)o[c * 8 + e];
+    dst[c] = __builtin_bit_cast(uint4, hv);
+  }
+}
+
+void check_hip(hipError_t e, const char* what) {
+  if (e != hipSuccess) throw Error(T0H_ERR_HIP, std::string(what) + ": " + hipGetErrorString(e));
+}
+
+void check_common(const AttnDesc& d) {
+  if (!d.qkv || !d.out || !d.grp || !d.q_norm || !d.k_norm) throw Error(T0H_ERR_INVALID_ARG, "attention: null pointer");
+  if (d.heads <= 0 || d.E != d.heads * HD)
+    throw Error(T0H_ERR_UNSUPPORTED, "attention: head_dim must be 64 (embed_dim = 64 * num_heads)");
+}
+
+}  // namespace
+
+void launch_time_attention(const AttnDesc& d, hipStream_t s) {
+  if (d.v <= 0 || d.p <= 0) return;
+  check_common(d);
+  if (!d.att || !d.fut || !d.rope_cos || !d.rope_sin || !d.rope_scale)
+    throw Error(T0H_ERR_INVALID_ARG, "time attention: null pointer");
+  if (d.p > T0H_MAX_PATCHES)
+    throw Error(T0H_ERR_UNSUPPORTED, "time attention: window of " + std::to_string(d.p) + " patches exceeds " +
+                                         std::to_string(T0H_MAX_PATCHES));
+  const size_t lds = time_attn_lds(d.p);
+  check_hip(hipFuncSetAttribute(reinterpret_cast<const void*>(&k_time_attn), hipFuncAttributeMaxDynamicSharedMemorySize,
+                                (int)lds),
+            "hipFuncSetAttribute(k_time_attn)");
+  hipLaunchKernelGGL(k_time_attn, dim3(d.v * d.heads), dim3(256), lds, s, d);
+  check_hip(hipGetLastError(), "k_time_attn launch");
+}
+
+void launch_group_attention(const AttnDesc& d, hipStream_t s) {
+  if (d.v <= 0 || d.p <= 0) return;
+  check_common(d);
+  if (!d.perm || !d.seg_begin || !d.seg_len) throw Error(T0H_ERR_INVALID_ARG, "group attention: null segment arrays");
+  const long long tasks = (long long)d.v * d.p * d.heads;
+  hipLaunchKernelGGL(k_group_attn, dim3((unsigned)((tasks + 255) / 256)), dim3(256), 0, s, d);
+  check_hip(hipGetLastError(), "k_group_attn launch");
+}
+
+}  // namespace t0h

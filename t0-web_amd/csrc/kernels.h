@@ -1,0 +1,129 @@
+// Host-callable launchers for the CDNA4 (gfx950) kernels of the t0hip engine.
+// Every launcher validates the shapes its kernel and grid assume before
+// launching and throws t0h::Error on a violation.
+#pragma once
+
+#include <hip/hip_runtime.h>
+
+#include <cstddef>
+#include <cstdint>
+
+namespace t0h {
+
+// ---- quantized / f16 GEMM --------------------------------------------------
+enum Epilogue {
+  EPI_STORE_F32 = 0,  // y = acc + bias (+ row_add[row_add_idx[m]]) (relu opt.), f32 out
+  EPI_STORE_F16 = 1,  // y = acc + bias (relu opt.), f16 out
+  EPI_RESID_F32 = 2,  // y += acc + bias, f32 in/out (residual stream)
+  EPI_SWIGLU_F16 = 3, // y[:, j] = silu(acc_j + b_j) * (acc_{H+j} + b_{H+j}), f16 out, N = H
+};
+
+struct GemmDesc {
+  int wtype = 0;              // T0H_F16 / T0H_Q8_0 / T0H_Q4_0
+  const void* w = nullptr;    // weight rows [N_w, K] in GGUF layout
+  const void* a = nullptr;    // activations [M, K], row stride lda elements
+  int a_f32 = 0;              // 1: a is float, 0: a is _Float16
+  int lda = 0;
+  const float* bias = nullptr;  // [N_w] or null
+  void* y = nullptr;          // output, row stride ldy elements
+  int ldy = 0;
+  int M = 0, N = 0, K = 0;    // N = output columns (EPI_SWIGLU_F16: H; weight rows are 2H)
+  int relu = 0;
+  const float* row_add = nullptr;  // EPI_STORE_F32 only: [n_rows_table, N]
+  const int* row_add_idx = nullptr;
+  int epi = EPI_STORE_F32;
+};
+
+void launch_gemm(const GemmDesc& d, hipStream_t s);
+// force = 0: pick by M; 1: MFMA tile kernel; 2: bandwidth-bound small-M kernel.
+void launch_gemm_forced(const GemmDesc& d, int force, hipStream_t s);
+void launch_dequant(int type, const void* w, size_t n, float* out, hipStream_t s);
+
+// ---- norms -----------------------------------------------------------------
+// out_f16[r] = x[map ? map[r] : r] / sqrt(mean(x^2) + 1e-8) * scale
+void launch_rmsnorm(const float* x, const float* scale, _Float16* out, const int* row_map, int rows, int dim,
+                    hipStream_t s);
+
+// ---- attention ---------------------------------------------------------------
+struct AttnDesc {
+  const _Float16* qkv = nullptr;  // [v*p, 3E]
+  _Float16* out = nullptr;        // [v*p, E]
+  int v = 0, p = 0, E = 0, heads = 0;
+  const float* q_norm = nullptr;  // [head_dim]
+  const float* k_norm = nullptr;
+  const float* rope_cos = nullptr;  // [p, head_dim]
+  const float* rope_sin = nullptr;
+  const float* rope_scale = nullptr;
+  const int* grp = nullptr;          // [v*p] patch group id (-1 = all-PAD patch)
+  const uint8_t* att = nullptr;      // [v*p] patch attendable
+  const uint8_t* fut = nullptr;      // [v] row is FUTURE (bidirectional time attention)
+  // group attention: rows of each row's group, as a permutation + per-row segment
+  const int* perm = nullptr;         // [v]
+  const int* seg_begin = nullptr;    // [v]
+  const int* seg_len = nullptr;      // [v]
+};
+void launch_time_attention(const AttnDesc& d, hipStream_t s);
+void launch_group_attention(const AttnDesc& d, hipStream_t s);
+
+// ---- host-prep on device -------------------------------------------------------
+// A forecast window (data.rs from_context/pad + lib.rs:208-236 ragged rows) described per row:
+// steps [0,pad_left) PAD | [pad_left, pad_left+t_ctx): `lead` PAD then the row's `len` raw
+// values (NaN = MISSING) | then horizon + right padding WITHHELD.
+struct WindowDesc {
+  const float* ctx = nullptr;        // raw values, flat
+  const int64_t* src_off = nullptr;  // [v] offset of row r's first value in ctx
+  const int* len = nullptr;          // [v] values of row r
+  const int* group = nullptr;        // [v] row group id
+  int v = 0, t_ctx = 0, horizon = 0, pad_left = 0, t = 0, ps = 0;
+  int use_arcsinh = 1, variance_offset = 1;
+  float eps = 0.1f;
+};
+struct PatchOut {
+  _Float16* enc_in = nullptr;  // [v*p, 3*ps]
+  int* grp = nullptr;          // [v*p]
+  uint8_t* att = nullptr;      // [v*p]
+  int* type_idx = nullptr;     // [v*p] max(type, 0)
+  int* type_raw = nullptr;     // [v*p] reduced variate type (-1 = all PAD)
+  uint8_t* fut = nullptr;      // [v]
+  float* patch_loc = nullptr;  // [v*p] scaler loc at each patch's last step (may be null)
+  float* patch_scale = nullptr;
+};
+// Causal Welford scaler per row (scaler.rs:91-118), loc/scale per step into loc/scale [v*t].
+void launch_window_welford(const WindowDesc& w, float* loc, float* scale, hipStream_t s);
+// Patch encoder input + patch metadata from the window and its loc/scale.
+void launch_window_patchify(const WindowDesc& w, const float* loc, const float* scale, const PatchOut& o,
+                            hipStream_t s);
+// Same from an explicit (already padded and scaled) series on device.
+struct SeriesDev {
+  const float* variates = nullptr;
+  const int8_t* mask = nullptr;
+  const int64_t* group_ids = nullptr;
+  const int64_t* variate_type = nullptr;
+  int v = 0, t = 0, ps = 0;
+};
+void launch_series_patchify(const SeriesDev& sd, const PatchOut& o, hipStream_t s);
+void launch_fut_rows(const int* type_raw, uint8_t* fut, int v, int p, hipStream_t s);
+
+// ---- outputs ---------------------------------------------------------------------
+// Raw quantile head over rows x patch steps: out[r, k, q] (forward's [v,p,ps,nq]).
+void launch_quantile_head(const float* dec, float* out, int rows, int ps, int nq, hipStream_t s);
+// Forecast output: dec rows are (r, hp) pairs; applies the quantile head, sinh/rescale with
+// the loc/scale of patch (ctx_p-1+hp) and writes out[r, hp*ps+k, q] for steps < horizon.
+struct ForecastOutDesc {
+  const float* dec = nullptr;  // [v*hp, ps*nq]
+  const float* patch_loc = nullptr;
+  const float* patch_scale = nullptr;
+  float* out = nullptr;  // [v, horizon, nq]
+  int v = 0, p = 0, ctx_p = 0, hp = 0, ps = 0, nq = 0, horizon = 0, use_arcsinh = 1;
+};
+void launch_forecast_out(const ForecastOutDesc& d, hipStream_t s);
+// Decoder row gather map: map[r*hp + h] = r*p + ctx_p - 1 + h
+void launch_gather_map(int* map, int v, int p, int ctx_p, int hp, hipStream_t s);
+// AR window update: ctx[r, :] <- (ctx[r, horizon:] ++ out[r, :, q_idx]) trailing t_ctx values.
+void launch_ar_shift(float* ctx_next, const float* ctx, const float* out, int v, int t_ctx, int horizon, int nq,
+                     int q_idx, hipStream_t s);
+// Strided copy of one AR step's output into the [v, steps*horizon, nq] result.
+void launch_ar_store(float* dst, const float* step_out, int v, int horizon, int nq, int steps, int step,
+                     hipStream_t s);
+
+}  // namespace t0h

@@ -1,0 +1,333 @@
+// Fused element-wise / row kernels around the GEMMs: RMSNorm, on-device host
+// prep (padding, causal scaler, patch encoder input, patch metadata), the
+// quantile head with rescale + forecast slice, and the AR window update.
+#include <hip/hip_runtime.h>
+
+#include <string>
+
+#include "kernels.h"
+#include "t0hip_internal.h"
+
+namespace t0h {
+namespace {
+
+typedef _Float16 half4 __attribute__((ext_vector_type(4)));
+
+void check_hip(hipError_t e, const char* what) {
+  if (e != hipSuccess) throw Error(T0H_ERR_HIP, std::string(what) + ": " + hipGetErrorString(e));
+}
+
+// ---- RMSNorm (ops.rs:12-17; rmsnorm_full.wgsl): one wave per row ------------------
+__global__ __launch_bounds__(256) void k_rmsnorm(const float* x, const float* scale, _Float16* out, const int* map,
+                                                 int rows, int dim) {
+  const int lane = threadIdx.x & 63;
+  const int row = blockIdx.x * 4 + (threadIdx.x >> 6);
+  if (row >= rows) return;
+  const float* src = x + (size_t)(map ? map[row] : row) * dim;
+  float ss = 0.0f;
+  for (int c = lane * 4; c < dim; c += 256) {
+    const float4 v = *reinterpret_cast<const float4*>(src + c);
+    ss += v.x * v.x + v.y * v.y + v.z * v.z + v.w * v.w;
+  }
+#pragma unroll
+  for (int m = 32; m >= 1; m >>= 1) ss += __shfl_xor(ss, m);
+  const float denom = sqrtf(ss / (float)dim + 1e-8f);
+  _Float16* dst = out + (size_t)row * dim;
+  for (int c = lane * 4; c < dim; c += 256) {
+    const float4 v = *reinterpret_cast<const float4*>(src + c);
+    const float4 s = *reinterpret_cast<const float4*>(scale + c);
+    const half4 h = {(_Float16)((v.x / denom) * s.x), (_Float16)((v.y / denom) * s.y), (_Float16)((v.z / denom) * s.z),
+                     (_Float16)((v.w / denom) * s.w)};
+    *reinterpret_cast<half4*>(dst + c) = h;
+  }
+}
+
+// ---- forecast window (data.rs:52-155 + lib.rs:208-236) ------------------------------
+struct Step {
+  float x;
+  int mask, group, type;
+};
+__device__ __forceinline__ Step window_step(const WindowDesc& w, int r, int s) {
+  Step st{0.0f, T0H_MASK_PAD, -1, -1};
+  if (s < w.pad_left) return st;  // left padding to a patch boundary (data.rs:112, 118-122)
+  const int c = s - w.pad_left;
+  const int g = w.group[r];
+  if (c < w.t_ctx) {
+    const int lead = w.t_ctx - w.len[r];  // ragged rows start late (lib.rs:215-216)
+    if (c < lead) return st;
+    const float x = w.ctx[w.src_off[r] + (c - lead)];
+    st.group = g;
+    st.type = T0H_VT_TARGET;
+    if (isnan(x)) {
+      st.mask = T0H_MASK_MISSING;  // data.rs:64-66
+    } else {
+      st.x = x;
+      st.mask = T0H_MASK_VALID;
+    }
+    return st;
+  }
+  // horizon and its right padding: WITHHELD target steps (data.rs:72-76, 136-144)
+  st.group = g;
+  st.type = T0H_VT_TARGET;
+  st.mask = T0H_MASK_WITHHELD;
+  return st;
+}
+
+// scaler.rs:91-118 causal_row_stats, one thread per row.  Every operation is an
+// explicitly rounded IEEE op so no multiply-add is fused (Rust never contracts).
+__global__ __launch_bounds__(64) void k_welford(const WindowDesc w, float* loc, float* scale) {
+  const int r = blockIdx.x * 64 + threadIdx.x;
+  if (r >= w.v) return;
+  float count = 0.0f, mean = 0.0f, m2 = 0.0f;
+  const size_t base = (size_t)r * w.t;
+  for (int s = 0; s < w.t; ++s) {
+    const Step st = window_step(w, r, s);
+    if (st.mask == T0H_MASK_VALID) {
+      count = __fadd_rn(count, 1.0f);
+      const float delta = __fsub_rn(st.x, mean);
+      mean = __fadd_rn(mean, __fdiv_rn(delta, count));
+      const float delta2 = __fsub_rn(st.x, mean);
+      m2 = __fadd_rn(m2, __fmul_rn(delta, delta2));
+    }
+    const float var = count > 1.0f ? fmaxf(__fdiv_rn(m2, __fsub_rn(count, 1.0f)), 0.0f) : 0.0f;
+    float sc = w.variance_offset ? __fsqrt_rn(__fadd_rn(var, w.eps)) : fmaxf(__fsqrt_rn(var), w.eps);
+    float lc = mean;
+    if (st.group < 0) {  // padding sentinel (scaler.rs:56-62)
+      lc = 0.0f;
+      sc = 1.0f;
+    }
+    loc[base + s] = lc;
+    scale[base + s] = sc;
+  }
+}
+
+// Rust 1.99 std f32::asinh: ln_1p(ax + ax / (hypot(1, 1/ax) + 1/ax)) with x's sign.
+__device__ __forceinline__ float rust_asinh(float x) {
+  const float ax = fabsf(x);
+  const float ix = __fdiv_rn(1.0f, ax);
+  return copysignf(log1pf(__fadd_rn(ax, __fdiv_rn(ax, __fadd_rn(hypotf(1.0f, ix), ix)))), x);
+}
+
+struct PatchAcc {
+  int grp = -1, type = -1;
+  bool found = false, any = false;
+  __device__ void add(int mask, int group, int type_) {
+    if (mask != T0H_MASK_PAD) {
+      any = true;
+      if (!found) {  // mask.rs:12-28: first non-PAD step's value
+        found = true;
+        grp = group;
+        type = type_;
+      }
+    }
+  }
+};
+
+__device__ __forceinline__ void write_patch_meta(const PatchOut& o, size_t m, const PatchAcc& a) {
+  o.grp[m] = a.grp;
+  o.type_raw[m] = a.type;
+  o.type_idx[m] = a.type > 0 ? a.type : 0;  // model.rs:205 max(type, 0)
+  o.att[m] = a.any ? 1 : 0;                 // mask.rs:32-43
+}
+
+// One thread per (row, patch): scaled values (scaler.rs:80-84) + [vals | k/ps | valid]
+// encoder input (model.rs:185-197) + patch metadata + loc/scale at the patch end.
+__global__ __launch_bounds__(256) void k_window_patchify(const WindowDesc w, const float* loc, const float* scale,
+                                                         const PatchOut o) {
+  const int p = w.t / w.ps;
+  const long long m = (long long)blockIdx.x * 256 + threadIdx.x;
+  if (m >= (long long)w.v * p) return;
+  const int r = (int)(m / p), pi = (int)(m % p), ps = w.ps;
+  _Float16* enc = o.enc_in + m * 3 * ps;
+  PatchAcc acc;
+  for (int k = 0; k < ps; ++k) {
+    const int s = pi * ps + k;
+    const Step st = window_step(w, r, s);
+    acc.add(st.mask, st.group, st.type);
+    const size_t ti = (size_t)r * w.t + s;
+    const float z = __fdiv_rn(__fsub_rn(st.x, loc[ti]), scale[ti]);
+    const float val = w.use_arcsinh ? rust_asinh(z) : z;
+    enc[k] = (_Float16)val;
+    enc[ps + k] = (_Float16)((float)k / (float)ps);
+    enc[2 * ps + k] = (_Float16)(st.mask == T0H_MASK_VALID ? 1.0f : 0.0f);
+  }
+  write_patch_meta(o, m, acc);
+  if (o.patch_loc) {
+    const size_t te = (size_t)r * w.t + pi * ps + ps - 1;
+    o.patch_loc[m] = loc[te];
+    o.patch_scale[m] = scale[te];
+  }
+}
+
+__global__ __launch_bounds__(256) void k_series_patchify(const SeriesDev sd, const PatchOut o) {
+  const int p = sd.t / sd.ps;
+  const long long m = (long long)blockIdx.x * 256 + threadIdx.x;
+  if (m >= (long long)sd.v * p) return;
+  const int r = (int)(m / p), pi = (int)(m % p), ps = sd.ps;
+  _Float16* enc = o.enc_in + m * 3 * ps;
+  PatchAcc acc;
+  for (int k = 0; k < ps; ++k) {
+    const size_t src = (size_t)r * sd.t + pi * ps + k;
+    const int mask = sd.mask[src];
+    acc.add(mask, (int)sd.group_ids[src], (int)sd.variate_type[src]);
+    enc[k] = (_Float16)sd.variates[src];
+    enc[ps + k] = (_Float16)((float)k / (float)ps);
+    enc[2 * ps + k] = (_Float16)(mask == T0H_MASK_VALID ? 1.0f : 0.0f);
+  }
+  write_patch_meta(o, m, acc);
+}
+
+// mask.rs:52: a row is FUTURE (bidirectional) when its first patch's reduced type is FUTURE.
+__global__ void k_fut_rows(const int* type_raw, uint8_t* fut, int v, int p) {
+  const int r = blockIdx.x * 256 + threadIdx.x;
+  if (r < v) fut[r] = type_raw[(size_t)r * p] == T0H_VT_FUTURE ? 1 : 0;
+}
+
+// quantile_head.wgsl / ops.rs:195-210: q0 = raw0, q_i = q_{i-1} + log(1 + exp(raw_i))
+__device__ __forceinline__ float softplus(float x) { return logf(1.0f + expf(x)); }
+
+__global__ __launch_bounds__(256) void k_quantile_head(const float* dec, float* out, int rows, int ps, int nq) {
+  const long long t = (long long)blockIdx.x * 256 + threadIdx.x;
+  if (t >= (long long)rows * ps) return;
+  const float* src = dec + t * nq;
+  float* dst = out + t * nq;
+  float run = src[0];
+  dst[0] = run;
+  for (int i = 1; i < nq; ++i) {
+    run = run + softplus(src[i]);
+    dst[i] = run;
+  }
+}
+
+// quantile head + rescale (scaler.rs:125-148) + forecast slice (lib.rs:75-96)
+__global__ __launch_bounds__(256) void k_forecast_out(const ForecastOutDesc d) {
+  const long long t = (long long)blockIdx.x * 256 + threadIdx.x;
+  if (t >= (long long)d.v * d.hp * d.ps) return;
+  const int k = (int)(t % d.ps);
+  const long long rh = t / d.ps;
+  const int hh = (int)(rh % d.hp), r = (int)(rh / d.hp);
+  const int step = hh * d.ps + k;
+  if (step >= d.horizon) return;
+  const size_t pm = (size_t)r * d.p + (d.ctx_p - 1 + hh);
+  const float lc = d.patch_loc[pm], sc = d.patch_scale[pm];
+  const float* src = d.dec + (size_t)rh * d.ps * d.nq + (size_t)k * d.nq;
+  float* dst = d.out + ((size_t)r * d.horizon + step) * d.nq;
+  float run = src[0];
+  for (int i = 0; i < d.nq; ++i) {
+    if (i > 0) run = run + softplus(src[i]);
+    const float u = d.use_arcsinh ? sinhf(run) : run;
+    dst[i] = u * sc + lc;
+  }
+}
+
+__global__ void k_gather_map(int* map, int v, int p, int ctx_p, int hp) {
+  const int t = blockIdx.x * 256 + threadIdx.x;
+  if (t >= v * hp) return;
+  map[t] = (t / hp) * p + ctx_p - 1 + (t % hp);
+}
+
+__global__ __launch_bounds__(256) void k_ar_shift(float* next, const float* ctx, const float* out, int v, int t_ctx,
+                                                  int horizon, int nq, int q_idx) {
+  const long long t = (long long)blockIdx.x * 256 + threadIdx.x;
+  if (t >= (long long)v * t_ctx) return;
+  const int r = (int)(t / t_ctx), i = (int)(t % t_ctx);
+  float x;
+  if (horizon >= t_ctx) {
+    x = out[((size_t)r * horizon + (horizon - t_ctx + i)) * nq + q_idx];
+  } else if (i < t_ctx - horizon) {
+    x = ctx[(size_t)r * t_ctx + i + horizon];
+  } else {
+    x = out[((size_t)r * horizon + (i - (t_ctx - horizon))) * nq + q_idx];
+  }
+  next[t] = x;
+}
+
+__global__ __launch_bounds__(256) void k_ar_store(float* dst, const float* src, int v, int horizon, int nq, int steps,
+                                                  int step) {
+  const long long t = (long long)blockIdx.x * 256 + threadIdx.x;
+  const long long per = (long long)horizon * nq;
+  if (t >= (long long)v * per) return;
+  const int r = (int)(t / per);
+  const long long j = t % per;
+  dst[(size_t)r * steps * per + (size_t)step * per + j] = src[t];
+}
+
+unsigned blocks(long long n, int per) { return (unsigned)((n + per - 1) / per); }
+
+}  // namespace
+
+void launch_rmsnorm(const float* x, const float* scale, _Float16* out, const int* row_map, int rows, int dim,
+                    hipStream_t s) {
+  if (rows <= 0) return;
+  if (!x || !scale || !out) throw Error(T0H_ERR_INVALID_ARG, "rmsnorm: null pointer");
+  if (dim <= 0 || dim % 4) throw Error(T0H_ERR_UNSUPPORTED, "rmsnorm: dim must be a positive multiple of 4");
+  hipLaunchKernelGGL(k_rmsnorm, dim3(blocks(rows, 4)), dim3(256), 0, s, x, scale, out, row_map, rows, dim);
+  check_hip(hipGetLastError(), "k_rmsnorm launch");
+}
+
+void launch_window_welford(const WindowDesc& w, float* loc, float* scale, hipStream_t s) {
+  if (w.v <= 0) return;
+  if (!w.ctx || !w.src_off || !w.len || !w.group || !loc || !scale) throw Error(T0H_ERR_INVALID_ARG, "welford: null");
+  hipLaunchKernelGGL(k_welford, dim3(blocks(w.v, 64)), dim3(64), 0, s, w, loc, scale);
+  check_hip(hipGetLastError(), "k_welford launch");
+}
+
+void launch_window_patchify(const WindowDesc& w, const float* loc, const float* scale, const PatchOut& o,
+                            hipStream_t s) {
+  if (w.v <= 0) return;
+  if (w.ps <= 0 || w.t % w.ps) throw Error(T0H_ERR_SHAPE, "patchify: window not patch aligned");
+  if (!o.enc_in || !o.grp || !o.att || !o.type_idx || !o.type_raw) throw Error(T0H_ERR_INVALID_ARG, "patchify: null");
+  const long long n = (long long)w.v * (w.t / w.ps);
+  hipLaunchKernelGGL(k_window_patchify, dim3(blocks(n, 256)), dim3(256), 0, s, w, loc, scale, o);
+  check_hip(hipGetLastError(), "k_window_patchify launch");
+}
+
+void launch_series_patchify(const SeriesDev& sd, const PatchOut& o, hipStream_t s) {
+  if (sd.v <= 0) return;
+  if (sd.ps <= 0 || sd.t % sd.ps) throw Error(T0H_ERR_SHAPE, "patchify: series not patch aligned");
+  const long long n = (long long)sd.v * (sd.t / sd.ps);
+  hipLaunchKernelGGL(k_series_patchify, dim3(blocks(n, 256)), dim3(256), 0, s, sd, o);
+  check_hip(hipGetLastError(), "k_series_patchify launch");
+}
+
+void launch_fut_rows(const int* type_raw, uint8_t* fut, int v, int p, hipStream_t s) {
+  if (v <= 0) return;
+  hipLaunchKernelGGL(k_fut_rows, dim3(blocks(v, 256)), dim3(256), 0, s, type_raw, fut, v, p);
+  check_hip(hipGetLastError(), "k_fut_rows launch");
+}
+
+void launch_quantile_head(const float* dec, float* out, int rows, int ps, int nq, hipStream_t s) {
+  if (rows <= 0) return;
+  hipLaunchKernelGGL(k_quantile_head, dim3(blocks((long long)rows * ps, 256)), dim3(256), 0, s, dec, out, rows, ps, nq);
+  check_hip(hipGetLastError(), "k_quantile_head launch");
+}
+
+void launch_forecast_out(const ForecastOutDesc& d, hipStream_t s) {
+  if (d.v <= 0 || d.hp <= 0) return;
+  hipLaunchKernelGGL(k_forecast_out, dim3(blocks((long long)d.v * d.hp * d.ps, 256)), dim3(256), 0, s, d);
+  check_hip(hipGetLastError(), "k_forecast_out launch");
+}
+
+void launch_gather_map(int* map, int v, int p, int ctx_p, int hp, hipStream_t s) {
+  if (v <= 0 || hp <= 0) return;
+  hipLaunchKernelGGL(k_gather_map, dim3(blocks((long long)v * hp, 256)), dim3(256), 0, s, map, v, p, ctx_p, hp);
+  check_hip(hipGetLastError(), "k_gather_map launch");
+}
+
+void launch_ar_shift(float* ctx_next, const float* ctx, const float* out, int v, int t_ctx, int horizon, int nq,
+                     int q_idx, hipStream_t s) {
+  if (v <= 0 || t_ctx <= 0) return;
+  hipLaunchKernelGGL(k_ar_shift, dim3(blocks((long long)v * t_ctx, 256)), dim3(256), 0, s, ctx_next, ctx, out, v, t_ctx,
+                     horizon, nq, q_idx);
+  check_hip(hipGetLastError(), "k_ar_shift launch");
+}
+
+void launch_ar_store(float* dst, const float* step_out, int v, int horizon, int nq, int steps, int step,
+                     hipStream_t s) {
+  if (v <= 0 || horizon <= 0) return;
+  hipLaunchKernelGGL(k_ar_store, dim3(blocks((long long)v * horizon * nq, 256)), dim3(256), 0, s, dst, step_out, v,
+                     horizon, nq, steps, step);
+  check_hip(hipGetLastError(), "k_ar_store launch");
+}
+
+}  // namespace t0h

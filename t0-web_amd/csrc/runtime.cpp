@@ -1,0 +1,1117 @@
+// Host runtime of the t0hip engine: device context, resident GGUF weights,
+// per-model workspace and stream, the forward pass as a kernel sequence on
+// that stream, the forecast drivers, and every extern "C" entry point of
+// include/t0hip.h.
+//
+// Reference structure this replaces: crates/t0-fast/src/{engine.rs, pool.rs,
+// model.rs (GpuModel, forward_async), lib.rs (forecast entry points)}.
+#include <hip/hip_runtime.h>
+
+#include <algorithm>
+#include <cmath>
+#include <cstring>
+#include <memory>
+#include <numeric>
+#include <string>
+#include <unordered_map>
+#include <vector>
+
+#include "kernels.h"
+#include "t0hip_internal.h"
+
+namespace t0h {
+
+std::vector<uint8_t> synth_model_gguf(const t0h_synth_spec& s, int quant);
+std::vector<uint8_t> export_gguf(const uint8_t* bytes, size_t len, int quant);
+
+namespace {
+thread_local std::string g_last_error;
+
+void hip_check(hipError_t e, const char* what) {
+  if (e != hipSuccess) throw Error(T0H_ERR_HIP, std::string(what) + ": " + hipGetErrorString(e));
+}
+}  // namespace
+
+void set_error(const std::string& msg) { g_last_error = msg; }
+
+// ---------------------------------------------------------------------------
+// Resident model
+// ---------------------------------------------------------------------------
+struct Mat {
+  const void* w = nullptr;
+  int type = T0H_F16;
+  int n = 0, k = 0;
+  size_t bytes = 0;
+};
+struct RBlock {  // ops.rs:24-37 residual block
+  Mat hid, out, res;
+  const float *hb = nullptr, *ob = nullptr, *rb = nullptr;
+};
+struct Layer {
+  bool group = false;
+  Mat qkv, o, w0, w2;
+  const float *b_qkv, *b_o, *b0, *b2, *norm, *mlp_norm, *q_norm, *k_norm;
+};
+
+struct Buf {
+  void* p = nullptr;
+  size_t cap = 0;
+};
+
+// Pinned host staging for one upload stream-ordered on the model's stream; the
+// event marks when the last copy out of it has executed.
+struct Stage {
+  void* p = nullptr;
+  size_t cap = 0;
+  hipEvent_t ev = nullptr;
+  bool pending = false;
+};
+
+struct Workspace {
+  std::unordered_map<std::string, Buf> bufs;
+  std::unordered_map<std::string, Stage> stages;
+  uint64_t allocs = 0;
+  int rope_p = -1;
+};
+
+}  // namespace t0h
+
+struct t0h_ctx {
+  int device = 0;
+  std::string arch;
+};
+
+struct t0h_model {
+  t0h_ctx* ctx = nullptr;
+  t0h::ModelConfig mc;
+  hipStream_t stream = nullptr;
+  uint8_t* d_weights = nullptr;
+  size_t weights_bytes = 0;
+  uint64_t quantizable_bytes = 0;
+  t0h::RBlock enc, dec;
+  const float* type_emb = nullptr;
+  int n_types = 0;
+  const float* out_norm = nullptr;
+  std::vector<t0h::Layer> layers;
+  t0h::Workspace ws;
+};
+
+namespace t0h {
+namespace {
+
+// ---- workspace (grow-only, like pool.rs:75-93) ----
+template <typename T>
+T* ws_get(t0h_model* m, const char* name, size_t count) {
+  Buf& b = m->ws.bufs[name];
+  const size_t bytes = std::max<size_t>(count * sizeof(T), 256);
+  if (b.cap < bytes) {
+    if (b.p) {
+      hip_check(hipStreamSynchronize(m->stream), "hipStreamSynchronize");
+      hip_check(hipFree(b.p), "hipFree");
+      b.p = nullptr;
+      b.cap = 0;
+    }
+    const size_t want = bytes + bytes / 4;
+    if (hipMalloc(&b.p, want) != hipSuccess) {
+      (void)hipGetLastError();
+      throw Error(T0H_ERR_OOM, std::string("device allocation of ") + std::to_string(want) + " bytes failed (" + name + ")");
+    }
+    b.cap = want;
+    m->ws.allocs++;
+  }
+  return static_cast<T*>(b.p);
+}
+
+// Copy n host elements into device buffer `name` (grown as needed), stream-ordered.
+// The host data is first copied into a pinned staging buffer owned by the model, so
+// the caller's memory may be released as soon as this returns.
+template <typename T>
+T* put(t0h_model* m, const char* name, const T* src, size_t n) {
+  T* dst = ws_get<T>(m, name, n);
+  if (n == 0) return dst;
+  const size_t bytes = n * sizeof(T);
+  Stage& st = m->ws.stages[name];
+  if (st.pending) {
+    hip_check(hipEventSynchronize(st.ev), "hipEventSynchronize");
+    st.pending = false;
+  }
+  if (!st.ev) hip_check(hipEventCreateWithFlags(&st.ev, hipEventDisableTiming), "hipEventCreate");
+  if (st.cap < bytes) {
+    if (st.p) hip_check(hipHostFree(st.p), "hipHostFree");
+    st.p = nullptr;
+    st.cap = 0;
+    if (hipHostMalloc(&st.p, bytes + bytes / 4, hipHostMallocDefault) != hipSuccess) {
+      (void)hipGetLastError();
+      throw Error(T0H_ERR_OOM, "pinned host allocation failed");
+    }
+    st.cap = bytes + bytes / 4;
+  }
+  std::memcpy(st.p, src, bytes);
+  hip_check(hipMemcpyAsync(dst, st.p, bytes, hipMemcpyHostToDevice, m->stream), "hipMemcpyAsync H2D");
+  hip_check(hipEventRecord(st.ev, m->stream), "hipEventRecord");
+  st.pending = true;
+  return dst;
+}
+template <typename T>
+void download(t0h_model* m, T* dst, const T* src, size_t n) {
+  if (n) hip_check(hipMemcpyAsync(dst, src, n * sizeof(T), hipMemcpyDeviceToHost, m->stream), "hipMemcpyAsync D2H");
+}
+void sync(t0h_model* m) { hip_check(hipStreamSynchronize(m->stream), "hipStreamSynchronize"); }
+
+// ---- load ----
+size_t align256(size_t x) { return (x + 255) & ~size_t(255); }
+
+struct Placement {
+  const GgufTensor* t;
+  bool as_matrix;  // device keeps GGUF blocks/f16 rows; else f32 vector
+  int dev_type;
+  size_t off, bytes;
+};
+
+void load_model(t0h_model* m, const uint8_t* bytes, size_t len) {
+  GgufFile f = read_gguf(bytes, len);
+  m->mc = config_from_meta(f);
+  const t0h_config& c = m->mc.c;
+  validate_model(f, c);
+  if (c.embed_dim / c.num_heads != 64)
+    throw Error(T0H_ERR_UNSUPPORTED, "this engine's attention kernels require head_dim 64");
+  if (c.embed_dim % 64 || c.mlp_hidden_dim % 64 || (3 * c.patch_size) % 32)
+    throw Error(T0H_ERR_UNSUPPORTED, "embed_dim and mlp_hidden_dim must be multiples of 64 and 3*patch_size of 32");
+
+  std::vector<std::string> matrices = {"patch_encoder.projection.mlp.hidden_layer.weight",
+                                       "patch_encoder.projection.mlp.output_layer.weight",
+                                       "patch_encoder.projection.residual_layer.weight",
+                                       "decoder.mlp.hidden_layer.weight",
+                                       "decoder.mlp.output_layer.weight",
+                                       "decoder.residual_layer.weight"};
+  std::vector<std::string> vectors = {"patch_encoder.projection.mlp.hidden_layer.bias",
+                                      "patch_encoder.projection.mlp.output_layer.bias",
+                                      "patch_encoder.projection.residual_layer.bias",
+                                      "patch_encoder.type_embeddings.weight",
+                                      "transformer.out_norm.scale",
+                                      "decoder.mlp.hidden_layer.bias",
+                                      "decoder.mlp.output_layer.bias",
+                                      "decoder.residual_layer.bias"};
+  const std::vector<bool> types = layer_types(c);
+  for (size_t i = 0; i < types.size(); ++i) {
+    const std::string p = "transformer.layers." + std::to_string(i);
+    for (const char* s : {".attention_block.attention.wQKV.weight", ".attention_block.attention.wO.weight",
+                          ".mlp.0.weight", ".mlp.2.weight"})
+      matrices.push_back(p + s);
+    for (const char* s : {".attention_block.norm.scale", ".attention_block.attention.wQKV.bias",
+                          ".attention_block.attention.wO.bias", ".attention_block.attention.q_norm.scale",
+                          ".attention_block.attention.k_norm.scale", ".norm.scale", ".mlp.0.bias", ".mlp.2.bias"})
+      vectors.push_back(p + s);
+  }
+  std::unordered_map<std::string, Placement> place;
+  size_t off = 0;
+  for (const auto& n : matrices) {
+    const GgufTensor& t = f.tensors.at(n);
+    Placement pl{&t, true, t.type == T0H_F32 ? T0H_F16 : t.type, off, 0};
+    pl.bytes = t.type == T0H_F32 ? t.n * 2 : t.nbytes;
+    off = align256(off + pl.bytes);
+    place[n] = pl;
+  }
+  for (const auto& n : vectors) {
+    const GgufTensor& t = f.tensors.at(n);
+    Placement pl{&t, false, T0H_F32, off, t.n * 4};
+    off = align256(off + pl.bytes);
+    place[n] = pl;
+  }
+  std::vector<uint8_t> host(off, 0);
+  for (auto& kv : place) {
+    const Placement& pl = kv.second;
+    uint8_t* dst = host.data() + pl.off;
+    if (!pl.as_matrix) {
+      dequantize(pl.t->type, pl.t->data, pl.t->n, reinterpret_cast<float*>(dst));
+    } else if (pl.t->type == T0H_F32) {  // f32 matrices are held as f16 rows
+      std::vector<float> tmp(pl.t->n);
+      std::memcpy(tmp.data(), pl.t->data, pl.t->n * 4);
+      quantize(T0H_F16, tmp.data(), tmp.size(), dst);
+    } else {
+      std::memcpy(dst, pl.t->data, pl.t->nbytes);  // GGUF blocks verbatim
+    }
+  }
+  if (hipMalloc(&m->d_weights, off) != hipSuccess) {
+    (void)hipGetLastError();
+    throw Error(T0H_ERR_OOM, "device allocation for weights failed");
+  }
+  m->weights_bytes = off;
+  hip_check(hipMemcpy(m->d_weights, host.data(), off, hipMemcpyHostToDevice), "hipMemcpy weights");
+
+  auto mat = [&](const std::string& n) {
+    const Placement& pl = place.at(n);
+    Mat x;
+    x.w = m->d_weights + pl.off;
+    x.type = pl.dev_type;
+    x.n = (int)pl.t->shape[0];
+    x.k = (int)pl.t->shape[1];
+    x.bytes = pl.bytes;
+    return x;
+  };
+  auto vec = [&](const std::string& n) { return reinterpret_cast<const float*>(m->d_weights + place.at(n).off); };
+  auto rblock = [&](const std::string& p) {
+    RBlock b;
+    b.hid = mat(p + ".mlp.hidden_layer.weight");
+    b.out = mat(p + ".mlp.output_layer.weight");
+    b.res = mat(p + ".residual_layer.weight");
+    b.hb = vec(p + ".mlp.hidden_layer.bias");
+    b.ob = vec(p + ".mlp.output_layer.bias");
+    b.rb = vec(p + ".residual_layer.bias");
+    return b;
+  };
+  m->enc = rblock("patch_encoder.projection");
+  m->dec = rblock("decoder");
+  if (m->enc.hid.n % 64 || m->dec.hid.n % 64)
+    throw Error(T0H_ERR_UNSUPPORTED, "residual-block hidden widths must be multiples of 64");
+  m->type_emb = vec("patch_encoder.type_embeddings.weight");
+  m->n_types = (int)f.tensors.at("patch_encoder.type_embeddings.weight").shape[0];
+  m->out_norm = vec("transformer.out_norm.scale");
+  m->quantizable_bytes = 0;
+  for (size_t i = 0; i < types.size(); ++i) {
+    const std::string p = "transformer.layers." + std::to_string(i);
+    Layer L;
+    L.group = types[i];
+    L.qkv = mat(p + ".attention_block.attention.wQKV.weight");
+    L.o = mat(p + ".attention_block.attention.wO.weight");
+    L.w0 = mat(p + ".mlp.0.weight");
+    L.w2 = mat(p + ".mlp.2.weight");
+    L.b_qkv = vec(p + ".attention_block.attention.wQKV.bias");
+    L.b_o = vec(p + ".attention_block.attention.wO.bias");
+    L.b0 = vec(p + ".mlp.0.bias");
+    L.b2 = vec(p + ".mlp.2.bias");
+    L.norm = vec(p + ".attention_block.norm.scale");
+    L.mlp_norm = vec(p + ".norm.scale");
+    L.q_norm = vec(p + ".attention_block.attention.q_norm.scale");
+    L.k_norm = vec(p + ".attention_block.attention.k_norm.scale");
+    m->quantizable_bytes += L.qkv.bytes + L.o.bytes + L.w0.bytes + L.w2.bytes;
+    m->layers.push_back(L);
+  }
+}
+
+// ---- RoPE tables (ops.rs:77-116): f64 math, f32 tables, xpos halves-concat ----
+void rope_tables(int p, int hd, std::vector<float>& cs, std::vector<float>& sn, std::vector<float>& sc) {
+  cs.assign((size_t)p * hd, 0.f);
+  sn.assign((size_t)p * hd, 0.f);
+  sc.assign((size_t)p * hd, 0.f);
+  const int half = hd / 2;
+  const double theta = 10000.0, scale_base = 512.0;
+  const double max_half = std::floor((double)(p - 1) / 2.0);
+  for (int pos = 0; pos < p; ++pos) {
+    const double power = ((double)pos - max_half) / scale_base;
+    for (int j = 0; j < half; ++j) {
+      const double inv_freq = 1.0 / std::pow(theta, (double)(2 * j) / (double)hd);
+      const double angle = (double)pos * inv_freq;
+      const double base = (2.0 * j + 0.4 * hd) / (1.4 * hd);
+      const float s = (float)std::pow(base, power);
+      for (int k = 0; k < 2; ++k) {
+        cs[(size_t)pos * hd + 2 * j + k] = (float)std::cos(angle);
+        sn[(size_t)pos * hd + 2 * j + k] = (float)std::sin(angle);
+      }
+      sc[(size_t)pos * hd + j] = s;
+      sc[(size_t)pos * hd + half + j] = s;
+    }
+  }
+}
+
+// ---- group segments: rows sorted by group; per row its segment -------------
+void upload_segments(t0h_model* m, const std::vector<int64_t>& row_group, bool consistent) {
+  const int v = (int)row_group.size();
+  std::vector<int> perm(v), begin(v), len(v);
+  std::iota(perm.begin(), perm.end(), 0);
+  if (consistent) {
+    std::stable_sort(perm.begin(), perm.end(), [&](int a, int b) { return row_group[a] < row_group[b]; });
+    int i = 0;
+    while (i < v) {
+      int j = i;
+      while (j < v && row_group[perm[j]] == row_group[perm[i]]) ++j;
+      for (int k = i; k < j; ++k) {
+        begin[perm[k]] = i;
+        len[perm[k]] = j - i;
+      }
+      i = j;
+    }
+  } else {  // arbitrary per-patch groups: every row scans all rows (group equality is checked per key)
+    std::fill(begin.begin(), begin.end(), 0);
+    std::fill(len.begin(), len.end(), v);
+  }
+  put(m, "perm", perm.data(), v);
+  put(m, "seg_begin", begin.data(), v);
+  put(m, "seg_len", len.data(), v);
+}
+
+void ensure_rope(t0h_model* m, int p) {
+  if (m->ws.rope_p == p) return;
+  std::vector<float> a, b, c;
+  rope_tables(p, 64, a, b, c);
+  put(m, "rope_cos", a.data(), a.size());
+  put(m, "rope_sin", b.data(), b.size());
+  put(m, "rope_scale", c.data(), c.size());
+  m->ws.rope_p = p;
+}
+
+GemmDesc gemm(const Mat& w, const void* a, int lda, const float* bias, void* y, int ldy, int M, int epi, int relu = 0) {
+  GemmDesc d;
+  d.wtype = w.type;
+  d.w = w.w;
+  d.a = a;
+  d.lda = lda;
+  d.bias = bias;
+  d.y = y;
+  d.ldy = ldy;
+  d.M = M;
+  d.N = epi == EPI_SWIGLU_F16 ? w.n / 2 : w.n;
+  d.K = w.k;
+  d.relu = relu;
+  d.epi = epi;
+  return d;
+}
+
+struct PatchMeta {
+  _Float16* enc_in;
+  int *grp, *type_idx, *type_raw;
+  uint8_t *att, *fut;
+  float *patch_loc, *patch_scale;
+};
+
+PatchMeta patch_buffers(t0h_model* m, int v, int p) {
+  const size_t M = (size_t)v * p;
+  const int ps = (int)m->mc.c.patch_size;
+  PatchMeta pm;
+  pm.enc_in = ws_get<_Float16>(m, "enc_in", M * 3 * ps);
+  pm.grp = ws_get<int>(m, "grp", M);
+  pm.type_idx = ws_get<int>(m, "type_idx", M);
+  pm.type_raw = ws_get<int>(m, "type_raw", M);
+  pm.att = ws_get<uint8_t>(m, "att", M);
+  pm.fut = ws_get<uint8_t>(m, "fut", v);
+  pm.patch_loc = ws_get<float>(m, "patch_loc", M);
+  pm.patch_scale = ws_get<float>(m, "patch_scale", M);
+  return pm;
+}
+
+// Patch encoder + transformer layers (t0-fast model.rs:727-786 ≡ t0-core model.rs:184-229).
+// Expects enc_in / patch metadata / segments in the workspace.  Leaves the f32
+// residual stream in "x".
+void encode_and_layers(t0h_model* m, int v, int p, const PatchMeta& pm, float* trace_pe, float* trace_l0) {
+  const t0h_config& c = m->mc.c;
+  const int E = (int)c.embed_dim, ps = (int)c.patch_size, M = v * p;
+  const int H = (int)c.mlp_hidden_dim;
+  hipStream_t s = m->stream;
+  const int wide = std::max(E, m->enc.hid.n);
+  float* x = ws_get<float>(m, "x", (size_t)M * E);
+  _Float16* xn = ws_get<_Float16>(m, "xn", (size_t)M * wide);
+  _Float16* qkv = ws_get<_Float16>(m, "qkv", (size_t)M * 3 * E);
+  _Float16* hb = ws_get<_Float16>(m, "h", (size_t)M * H);
+  const int* perm = ws_get<int>(m, "perm", v);
+  const int* seg_begin = ws_get<int>(m, "seg_begin", v);
+  const int* seg_len = ws_get<int>(m, "seg_len", v);
+  ensure_rope(m, p);
+
+  // patch encoder residual block + type embedding (model.rs:199-207)
+  launch_gemm(gemm(m->enc.hid, pm.enc_in, 3 * ps, m->enc.hb, xn, m->enc.hid.n, M, EPI_STORE_F16, 1), s);
+  GemmDesc rd = gemm(m->enc.res, pm.enc_in, 3 * ps, m->enc.rb, x, E, M, EPI_STORE_F32);
+  rd.row_add = m->type_emb;
+  rd.row_add_idx = pm.type_idx;
+  launch_gemm(rd, s);
+  launch_gemm(gemm(m->enc.out, xn, m->enc.hid.n, m->enc.ob, x, E, M, EPI_RESID_F32), s);
+  if (trace_pe) download(m, trace_pe, x, (size_t)M * E);
+
+  AttnDesc ad;
+  ad.qkv = qkv;
+  ad.out = xn;
+  ad.v = v;
+  ad.p = p;
+  ad.E = E;
+  ad.heads = (int)c.num_heads;
+  ad.rope_cos = ws_get<float>(m, "rope_cos", (size_t)p * 64);
+  ad.rope_sin = ws_get<float>(m, "rope_sin", (size_t)p * 64);
+  ad.rope_scale = ws_get<float>(m, "rope_scale", (size_t)p * 64);
+  ad.grp = pm.grp;
+  ad.att = pm.att;
+  ad.fut = pm.fut;
+  ad.perm = perm;
+  ad.seg_begin = seg_begin;
+  ad.seg_len = seg_len;
+  for (size_t li = 0; li < m->layers.size(); ++li) {
+    const Layer& L = m->layers[li];
+    launch_rmsnorm(x, L.norm, xn, nullptr, M, E, s);
+    launch_gemm(gemm(L.qkv, xn, E, L.b_qkv, qkv, 3 * E, M, EPI_STORE_F16), s);
+    ad.q_norm = L.q_norm;
+    ad.k_norm = L.k_norm;
+    if (L.group)
+      launch_group_attention(ad, s);
+    else
+      launch_time_attention(ad, s);
+    launch_gemm(gemm(L.o, xn, E, L.b_o, x, E, M, EPI_RESID_F32), s);
+    launch_rmsnorm(x, L.mlp_norm, xn, nullptr, M, E, s);
+    launch_gemm(gemm(L.w0, xn, E, L.b0, hb, H, M, EPI_SWIGLU_F16), s);
+    launch_gemm(gemm(L.w2, hb, H, L.b2, x, E, M, EPI_RESID_F32), s);
+    if (li == 0 && trace_l0) download(m, trace_l0, x, (size_t)M * E);
+  }
+}
+
+// out_norm + decoder residual block on `rows` rows of x (gathered through map, or all).
+float* decode_rows(t0h_model* m, int rows, const int* map) {
+  const t0h_config& c = m->mc.c;
+  const int E = (int)c.embed_dim, nout = m->dec.out.n;
+  hipStream_t s = m->stream;
+  const float* x = ws_get<float>(m, "x", 1);
+  _Float16* din = ws_get<_Float16>(m, "dec_in", (size_t)rows * E);
+  _Float16* dh = ws_get<_Float16>(m, "dec_h", (size_t)rows * m->dec.hid.n);
+  float* dout = ws_get<float>(m, "dec_out", (size_t)rows * nout);
+  launch_rmsnorm(x, m->out_norm, din, map, rows, E, s);
+  launch_gemm(gemm(m->dec.hid, din, E, m->dec.hb, dh, m->dec.hid.n, rows, EPI_STORE_F16, 1), s);
+  launch_gemm(gemm(m->dec.res, din, E, m->dec.rb, dout, nout, rows, EPI_STORE_F32), s);
+  launch_gemm(gemm(m->dec.out, dh, m->dec.hid.n, m->dec.ob, dout, nout, rows, EPI_RESID_F32), s);
+  return dout;
+}
+
+// ---- forecast window (lib.rs:50-97) on device ----
+struct WindowRows {
+  int t_ctx = 0, horizon = 0;
+  const float* d_ctx = nullptr;      // device
+  std::vector<int64_t> src_off;      // per row, into d_ctx
+  std::vector<int> len;              // per row
+  std::vector<int64_t> group;        // per row (>= 0)
+};
+
+void forecast_window(t0h_model* m, const WindowRows& wr, float* d_out) {
+  const t0h_config& c = m->mc.c;
+  const int ps = (int)c.patch_size, nq = (int)c.n_quantiles;
+  const int v = (int)wr.src_off.size();
+  if (v == 0) return;
+  if (wr.t_ctx <= 0) throw Error(T0H_ERR_INVALID_ARG, "forecast: context length must be positive");
+  const int pad_left = (ps - wr.t_ctx % ps) % ps;
+  const int padded_h = (wr.horizon + ps - 1) / ps * ps;
+  if (padded_h > T0H_MAX_HORIZON)
+    throw Error(T0H_ERR_HORIZON, "single-window forecast can't exceed max_horizon (1024) in one pass -- use forecast_rollout");
+  const int t = pad_left + wr.t_ctx + padded_h;
+  const int p = t / ps, ctx_p = (wr.t_ctx + pad_left) / ps, hp = padded_h / ps;
+  if (p > T0H_MAX_PATCHES)
+    throw Error(T0H_ERR_UNSUPPORTED, "window of " + std::to_string(p) + " patches exceeds " + std::to_string(T0H_MAX_PATCHES));
+  hipStream_t s = m->stream;
+
+  // dense group ids for the device
+  std::vector<int64_t> sorted(wr.group);
+  std::sort(sorted.begin(), sorted.end());
+  sorted.erase(std::unique(sorted.begin(), sorted.end()), sorted.end());
+  std::vector<int> dense(v);
+  std::vector<int64_t> dense64(v);
+  for (int r = 0; r < v; ++r) {
+    dense[r] = (int)(std::lower_bound(sorted.begin(), sorted.end(), wr.group[r]) - sorted.begin());
+    dense64[r] = dense[r];
+  }
+  const int64_t* d_off = put(m, "win_off", wr.src_off.data(), v);
+  const int* d_len = put(m, "win_len", wr.len.data(), v);
+  const int* d_grp = put(m, "win_grp", dense.data(), v);
+  upload_segments(m, dense64, true);
+
+  WindowDesc w;
+  w.ctx = wr.d_ctx;
+  w.src_off = d_off;
+  w.len = d_len;
+  w.group = d_grp;
+  w.v = v;
+  w.t_ctx = wr.t_ctx;
+  w.horizon = wr.horizon;
+  w.pad_left = pad_left;
+  w.t = t;
+  w.ps = ps;
+  w.use_arcsinh = c.scaler_use_arcsinh;
+  w.variance_offset = c.scaler_variance_offset;
+  w.eps = c.scaler_eps;
+  float* loc = ws_get<float>(m, "loc", (size_t)v * t);
+  float* scl = ws_get<float>(m, "scale", (size_t)v * t);
+  PatchMeta pm = patch_buffers(m, v, p);
+  launch_window_welford(w, loc, scl, s);
+  PatchOut po{pm.enc_in, pm.grp, pm.att, pm.type_idx, pm.type_raw, pm.fut, pm.patch_loc, pm.patch_scale};
+  launch_window_patchify(w, loc, scl, po, s);
+  launch_fut_rows(pm.type_raw, pm.fut, v, p, s);
+  encode_and_layers(m, v, p, pm, nullptr, nullptr);
+  if (hp == 0) return;
+  int* map = ws_get<int>(m, "dec_map", (size_t)v * hp);
+  launch_gather_map(map, v, p, ctx_p, hp, s);
+  float* dout = decode_rows(m, v * hp, map);
+  ForecastOutDesc od;
+  od.dec = dout;
+  od.patch_loc = pm.patch_loc;
+  od.patch_scale = pm.patch_scale;
+  od.out = d_out;
+  od.v = v;
+  od.p = p;
+  od.ctx_p = ctx_p;
+  od.hp = hp;
+  od.ps = ps;
+  od.nq = nq;
+  od.horizon = wr.horizon;
+  od.use_arcsinh = c.scaler_use_arcsinh;
+  launch_forecast_out(od, s);
+}
+
+void require(bool ok, const char* msg) {
+  if (!ok) throw Error(T0H_ERR_INVALID_ARG, msg);
+}
+
+void bind_device(const t0h_model* m) { hip_check(hipSetDevice(m->ctx->device), "hipSetDevice"); }
+
+float* upload_contexts(t0h_model* m, const float* ctx, size_t n) { return put(m, "ctx_in", ctx, n); }
+
+void check_out(size_t out_len, size_t want) {
+  if (out_len != want)
+    throw Error(T0H_ERR_INVALID_ARG, "output buffer holds " + std::to_string(out_len) + " floats, expected " + std::to_string(want));
+}
+
+// forecast_rollout helpers (quantile.rs:16-76)
+std::vector<float> interpolate_quantiles(const std::vector<float>& query, const float* levels_in, const float* values_in,
+                                         size_t nl) {
+  std::vector<size_t> idx(nl);
+  std::iota(idx.begin(), idx.end(), 0);
+  std::stable_sort(idx.begin(), idx.end(), [&](size_t a, size_t b) { return levels_in[a] < levels_in[b]; });
+  std::vector<float> lv, vv;
+  for (size_t i : idx) {
+    lv.push_back(levels_in[i]);
+    vv.push_back(values_in[i]);
+  }
+  if (lv.front() > 0.0f) {
+    lv.insert(lv.begin(), 0.0f);
+    vv.insert(vv.begin(), vv.front());
+  }
+  if (lv.back() < 1.0f) {
+    lv.push_back(1.0f);
+    vv.push_back(vv.back());
+  }
+  std::vector<float> out;
+  for (float q : query) {
+    size_t upper = std::upper_bound(lv.begin(), lv.end(), q) - lv.begin();  // partition_point(l <= q)
+    upper = std::min(upper, lv.size() - 1);
+    size_t lower = upper > 0 ? upper - 1 : 0;
+    const float diff = lv[upper] - lv[lower];
+    const float wt = diff == 0.0f ? 0.0f : (q - lv[lower]) / diff;
+    out.push_back(vv[lower] + wt * (vv[upper] - vv[lower]));
+  }
+  return out;
+}
+std::vector<float> weighted_quantile(const std::vector<float>& query, const std::vector<float>& weights,
+                                     const std::vector<float>& samples) {
+  float sum = 0.0f;
+  for (float w : weights) sum += w;
+  std::vector<size_t> idx(samples.size());
+  std::iota(idx.begin(), idx.end(), 0);
+  std::stable_sort(idx.begin(), idx.end(), [&](size_t a, size_t b) { return samples[a] < samples[b]; });
+  std::vector<float> ss, cw;
+  float cum = 0.0f;
+  for (size_t i : idx) {
+    ss.push_back(samples[i]);
+    cum += weights[i] / sum;
+    cw.push_back(std::min(1.0f, std::max(0.0f, cum)));
+  }
+  return interpolate_quantiles(query, cw.data(), ss.data(), ss.size());
+}
+std::vector<float> prob_mass(const float* levels, size_t n) {
+  std::vector<float> b(n + 2);
+  b[0] = 0.0f;
+  std::copy(levels, levels + n, b.begin() + 1);
+  b[n + 1] = 1.0f;
+  std::vector<float> mass(n);
+  float sum = 0.0f;
+  for (size_t i = 0; i < n; ++i) {
+    mass[i] = (b[i + 2] - b[i]) / 2.0f;
+    sum += mass[i];
+  }
+  for (float& x : mass) x /= sum;
+  return mass;
+}
+
+int median_index(const t0h_config& c) {
+  int best = 0;
+  for (int i = 1; i < (int)c.n_quantiles; ++i)
+    if (std::fabs(c.quantile_levels[i] - 0.5f) < std::fabs(c.quantile_levels[best] - 0.5f)) best = i;
+  return best;
+}
+
+}  // namespace
+
+// Exposed for the rollout driver.
+void forecast_host(t0h_model* m, const float* ctx, size_t v, size_t t_ctx, size_t horizon, float* out) {
+  const int nq = (int)m->mc.c.n_quantiles;
+  float* d_ctx = upload_contexts(m, ctx, v * t_ctx);
+  WindowRows wr;
+  wr.t_ctx = (int)t_ctx;
+  wr.horizon = (int)horizon;
+  wr.d_ctx = d_ctx;
+  for (size_t r = 0; r < v; ++r) {
+    wr.src_off.push_back((int64_t)(r * t_ctx));
+    wr.len.push_back((int)t_ctx);
+    wr.group.push_back(0);  // data.rs:57 one shared group id
+  }
+  float* d_out = ws_get<float>(m, "out", std::max<size_t>(1, v * horizon * nq));
+  forecast_window(m, wr, d_out);
+  download(m, out, d_out, v * horizon * nq);
+  sync(m);
+}
+
+void forecast_batch_host(t0h_model* m, const float* ctx, size_t n, size_t t_ctx, size_t horizon, size_t chunk,
+                         float* out) {
+  const int nq = (int)m->mc.c.n_quantiles;
+  chunk = (chunk == 0 || chunk > n) ? n : chunk;
+  float* d_ctx = upload_contexts(m, ctx, n * t_ctx);
+  float* d_out = ws_get<float>(m, "out", std::max<size_t>(1, n * horizon * nq));
+  for (size_t start = 0; start < n; start += chunk) {
+    const size_t k = std::min(chunk, n - start);
+    WindowRows wr;
+    wr.t_ctx = (int)t_ctx;
+    wr.horizon = (int)horizon;
+    wr.d_ctx = d_ctx;
+    for (size_t r = 0; r < k; ++r) {
+      wr.src_off.push_back((int64_t)((start + r) * t_ctx));
+      wr.len.push_back((int)t_ctx);
+      wr.group.push_back((int64_t)r);  // data.rs:96-105 distinct group per signal
+    }
+    forecast_window(m, wr, d_out + start * horizon * nq);
+  }
+  download(m, out, d_out, n * horizon * nq);
+  sync(m);
+}
+
+}  // namespace t0h
+
+using namespace t0h;
+
+#define API_BEGIN try {
+#define API_END                                    \
+  }                                                \
+  catch (const t0h::Error& e) {                    \
+    set_error(e.what());                           \
+    return e.code;                                 \
+  }                                                \
+  catch (const std::bad_alloc&) {                  \
+    set_error("host allocation failed");           \
+    return T0H_ERR_OOM;                            \
+  }                                                \
+  catch (const std::exception& e) {                \
+    set_error(std::string("internal error: ") + e.what()); \
+    return T0H_ERR_INVALID_ARG;                    \
+  }                                                \
+  return T0H_OK;
+
+extern "C" {
+
+const char* t0h_last_error(void) { return g_last_error.c_str(); }
+int t0h_abi_version(void) { return T0H_ABI_VERSION; }
+
+int t0h_ctx_create(int device, t0h_ctx** out) {
+  API_BEGIN
+  require(out != nullptr, "t0h_ctx_create: out is NULL");
+  *out = nullptr;
+  int n = 0;
+  if (hipGetDeviceCount(&n) != hipSuccess || n == 0) {
+    (void)hipGetLastError();
+    throw Error(T0H_ERR_NO_DEVICE, "no GPU device available");
+  }
+  if (device < 0 || device >= n) throw Error(T0H_ERR_NO_DEVICE, "device index out of range");
+  hip_check(hipSetDevice(device), "hipSetDevice");
+  hipDeviceProp_t prop;
+  hip_check(hipGetDeviceProperties(&prop, device), "hipGetDeviceProperties");
+  std::string arch = prop.gcnArchName;
+  if (arch.rfind("gfx950", 0) != 0)
+    throw Error(T0H_ERR_UNSUPPORTED, "this library is built for gfx950 (MI355X); device is " + arch);
+  auto* c = new t0h_ctx;
+  c->device = device;
+  c->arch = arch;
+  *out = c;
+  API_END
+}
+
+void t0h_ctx_destroy(t0h_ctx* ctx) { delete ctx; }
+
+int t0h_gguf_inspect(const uint8_t* bytes, size_t len, t0h_config* cfg, size_t* n_tensors) {
+  API_BEGIN
+  require(bytes != nullptr || len == 0, "t0h_gguf_inspect: bytes is NULL");
+  GgufFile f = read_gguf(bytes, len);
+  ModelConfig mc = config_from_meta(f);
+  validate_model(f, mc.c);
+  if (cfg) *cfg = mc.c;
+  if (n_tensors) *n_tensors = f.tensors.size();
+  API_END
+}
+
+int t0h_model_load_gguf(t0h_ctx* ctx, const uint8_t* bytes, size_t len, t0h_model** out) {
+  API_BEGIN
+  require(ctx && out, "t0h_model_load_gguf: NULL argument");
+  require(bytes != nullptr || len == 0, "t0h_model_load_gguf: bytes is NULL");
+  *out = nullptr;
+  hip_check(hipSetDevice(ctx->device), "hipSetDevice");
+  std::unique_ptr<t0h_model> m(new t0h_model);
+  m->ctx = ctx;
+  hip_check(hipStreamCreateWithFlags(&m->stream, hipStreamNonBlocking), "hipStreamCreate");
+  try {
+    load_model(m.get(), bytes, len);
+  } catch (...) {
+    if (m->d_weights) (void)hipFree(m->d_weights);
+    (void)hipStreamDestroy(m->stream);
+    throw;
+  }
+  *out = m.release();
+  API_END
+}
+
+void t0h_model_destroy(t0h_model* m) {
+  if (!m) return;
+  (void)hipSetDevice(m->ctx->device);
+  (void)hipStreamSynchronize(m->stream);
+  for (auto& kv : m->ws.bufs)
+    if (kv.second.p) (void)hipFree(kv.second.p);
+  for (auto& kv : m->ws.stages) {
+    if (kv.second.p) (void)hipHostFree(kv.second.p);
+    if (kv.second.ev) (void)hipEventDestroy(kv.second.ev);
+  }
+  if (m->d_weights) (void)hipFree(m->d_weights);
+  (void)hipStreamDestroy(m->stream);
+  delete m;
+}
+
+int t0h_model_config(const t0h_model* m, t0h_config* out) {
+  API_BEGIN
+  require(m && out, "t0h_model_config: NULL argument");
+  *out = m->mc.c;
+  out->num_layers = (uint32_t)m->layers.size();
+  API_END
+}
+
+int t0h_model_weight_bytes(const t0h_model* m, uint64_t* quantizable, uint64_t* total) {
+  API_BEGIN
+  require(m != nullptr, "t0h_model_weight_bytes: NULL model");
+  if (quantizable) *quantizable = m->quantizable_bytes;
+  if (total) *total = m->weights_bytes;
+  API_END
+}
+
+void* t0h_model_stream(const t0h_model* m) { return m ? (void*)m->stream : nullptr; }
+
+int t0h_model_workspace(const t0h_model* m, uint64_t* resident, uint64_t* allocs) {
+  API_BEGIN
+  require(m != nullptr, "t0h_model_workspace: NULL model");
+  uint64_t b = 0;
+  for (const auto& kv : m->ws.bufs) b += kv.second.cap;
+  if (resident) *resident = b;
+  if (allocs) *allocs = m->ws.allocs;
+  API_END
+}
+
+int t0h_forward(t0h_model* m, const t0h_series* sr, float* out, size_t out_len, float* trace_pe, float* trace_l0) {
+  API_BEGIN
+  require(m && sr && out, "t0h_forward: NULL argument");
+  require(sr->variates && sr->mask && sr->group_ids && sr->variate_type, "t0h_forward: NULL series array");
+  bind_device(m);
+  const t0h_config& c = m->mc.c;
+  const int ps = (int)c.patch_size, nq = (int)c.n_quantiles, E = (int)c.embed_dim;
+  if (sr->t % ps) throw Error(T0H_ERR_SHAPE, "series width must be patch-aligned");
+  const int v = (int)sr->v, t = (int)sr->t, p = t / ps;
+  check_out(out_len, (size_t)v * p * ps * nq);
+  if (v == 0 || p == 0) return T0H_OK;
+  if (p > T0H_MAX_PATCHES) throw Error(T0H_ERR_UNSUPPORTED, "series exceeds the maximum patch count");
+  const size_t n = (size_t)v * t;
+  for (size_t i = 0; i < n; ++i)
+    if (sr->variate_type[i] >= m->n_types) throw Error(T0H_ERR_INVALID_ARG, "variate type out of range of the type embeddings");
+  // dense group ids (negative stays padding) and the row-level grouping
+  std::vector<int64_t> g(sr->group_ids, sr->group_ids + n), keys;
+  for (int64_t x : g)
+    if (x >= 0) keys.push_back(x);
+  std::sort(keys.begin(), keys.end());
+  keys.erase(std::unique(keys.begin(), keys.end()), keys.end());
+  for (auto& x : g) x = x < 0 ? -1 : (int64_t)(std::lower_bound(keys.begin(), keys.end(), x) - keys.begin());
+  std::vector<int64_t> row_group(v, -1);
+  bool consistent = true;
+  for (int r = 0; r < v && consistent; ++r)
+    for (int i = 0; i < t; ++i) {
+      const size_t k = (size_t)r * t + i;
+      if (sr->mask[k] == T0H_MASK_PAD || g[k] < 0) continue;
+      if (row_group[r] < 0) row_group[r] = g[k];
+      else if (row_group[r] != g[k]) {
+        consistent = false;
+        break;
+      }
+    }
+  const float* dv = put(m, "s_var", sr->variates, n);
+  const int8_t* dm = put(m, "s_mask", sr->mask, n);
+  const int64_t* dg = put(m, "s_grp", g.data(), n);
+  const int64_t* dt = put(m, "s_type", sr->variate_type, n);
+  upload_segments(m, row_group, consistent);
+  PatchMeta pm = patch_buffers(m, v, p);
+  SeriesDev sd{dv, dm, dg, dt, v, t, ps};
+  PatchOut po{pm.enc_in, pm.grp, pm.att, pm.type_idx, pm.type_raw, pm.fut, nullptr, nullptr};
+  launch_series_patchify(sd, po, m->stream);
+  launch_fut_rows(pm.type_raw, pm.fut, v, p, m->stream);
+  encode_and_layers(m, v, p, pm, trace_pe, trace_l0);
+  const int M = v * p;
+  float* dout = decode_rows(m, M, nullptr);
+  float* q = ws_get<float>(m, "out", (size_t)M * ps * nq);
+  launch_quantile_head(dout, q, M * ps, 1, nq, m->stream);
+  download(m, out, q, (size_t)M * ps * nq);
+  sync(m);
+  (void)E;
+  API_END
+}
+
+int t0h_forecast(t0h_model* m, const float* context, size_t v, size_t t_ctx, size_t horizon, float* out,
+                 size_t out_len) {
+  API_BEGIN
+  require(m && context && out, "t0h_forecast: NULL argument");
+  require(v > 0 && t_ctx > 0, "t0h_forecast: v and t_ctx must be positive");
+  bind_device(m);
+  check_out(out_len, v * horizon * m->mc.c.n_quantiles);
+  forecast_host(m, context, v, t_ctx, horizon, out);
+  API_END
+}
+
+int t0h_forecast_batch_chunked(t0h_model* m, const float* contexts, size_t n, size_t t_ctx, size_t horizon,
+                               size_t chunk, float* out, size_t out_len) {
+  API_BEGIN
+  require(m && contexts && out, "t0h_forecast_batch_chunked: NULL argument");
+  require(t_ctx > 0, "t0h_forecast_batch_chunked: t_ctx must be positive");
+  bind_device(m);
+  check_out(out_len, n * horizon * m->mc.c.n_quantiles);
+  if (n == 0) return T0H_OK;
+  forecast_batch_host(m, contexts, n, t_ctx, horizon, chunk, out);
+  API_END
+}
+
+int t0h_forecast_batch_rows_chunked(t0h_model* m, const float* contexts, const size_t* lengths, size_t n,
+                                    size_t horizon, size_t chunk, float* out, size_t out_len) {
+  API_BEGIN
+  require(m && out && (lengths || n == 0), "t0h_forecast_batch_rows_chunked: NULL argument");
+  bind_device(m);
+  const size_t nq = m->mc.c.n_quantiles, ps = m->mc.c.patch_size;
+  check_out(out_len, n * horizon * nq);
+  if (n == 0) return T0H_OK;
+  size_t total = 0;
+  std::vector<int64_t> offs(n);
+  for (size_t i = 0; i < n; ++i) {
+    offs[i] = (int64_t)total;
+    total += lengths[i];
+  }
+  require(contexts || total == 0, "t0h_forecast_batch_rows_chunked: contexts is NULL");
+  chunk = (chunk == 0 || chunk > n) ? n : chunk;
+  float* d_ctx = upload_contexts(m, contexts, total);
+  float* d_out = ws_get<float>(m, "out", std::max<size_t>(1, n * horizon * nq));
+  for (size_t start = 0; start < n; start += chunk) {  // lib.rs:200-240
+    const size_t k = std::min(chunk, n - start);
+    size_t common = 0;
+    for (size_t r = 0; r < k; ++r) common = std::max(common, (lengths[start + r] + ps - 1) / ps * ps);
+    WindowRows wr;
+    wr.t_ctx = (int)common;
+    wr.horizon = (int)horizon;
+    wr.d_ctx = d_ctx;
+    for (size_t r = 0; r < k; ++r) {
+      wr.src_off.push_back(offs[start + r]);
+      wr.len.push_back((int)lengths[start + r]);
+      wr.group.push_back((int64_t)r);
+    }
+    forecast_window(m, wr, d_out + start * horizon * nq);
+  }
+  download(m, out, d_out, n * horizon * nq);
+  sync(m);
+  API_END
+}
+
+static void grouped_rows(WindowRows& wr, const int64_t* row_group, size_t n_rows, size_t t_ctx) {
+  for (size_t r = 0; r < n_rows; ++r) {
+    if (row_group[r] < 0) throw Error(T0H_ERR_INVALID_ARG, "group ids must be non-negative");
+    wr.src_off.push_back((int64_t)(r * t_ctx));
+    wr.len.push_back((int)t_ctx);
+    wr.group.push_back(row_group[r]);
+  }
+}
+
+int t0h_forecast_grouped(t0h_model* m, const float* contexts, const int64_t* row_group, size_t n_rows, size_t t_ctx,
+                         size_t horizon, float* out, size_t out_len) {
+  API_BEGIN
+  require(m && contexts && row_group && out, "t0h_forecast_grouped: NULL argument");
+  require(n_rows > 0 && t_ctx > 0, "t0h_forecast_grouped: n_rows and t_ctx must be positive");
+  bind_device(m);
+  const size_t nq = m->mc.c.n_quantiles;
+  check_out(out_len, n_rows * horizon * nq);
+  WindowRows wr;
+  wr.t_ctx = (int)t_ctx;
+  wr.horizon = (int)horizon;
+  wr.d_ctx = upload_contexts(m, contexts, n_rows * t_ctx);
+  grouped_rows(wr, row_group, n_rows, t_ctx);
+  float* d_out = ws_get<float>(m, "out", std::max<size_t>(1, n_rows * horizon * nq));
+  forecast_window(m, wr, d_out);
+  download(m, out, d_out, n_rows * horizon * nq);
+  sync(m);
+  API_END
+}
+
+int t0h_forecast_grouped_dev(t0h_model* m, const float* d_contexts, const int64_t* row_group, size_t n_rows,
+                             size_t t_ctx, size_t horizon, float* d_out) {
+  API_BEGIN
+  require(m && d_contexts && row_group && d_out, "t0h_forecast_grouped_dev: NULL argument");
+  require(n_rows > 0 && t_ctx > 0, "t0h_forecast_grouped_dev: n_rows and t_ctx must be positive");
+  bind_device(m);
+  WindowRows wr;
+  wr.t_ctx = (int)t_ctx;
+  wr.horizon = (int)horizon;
+  wr.d_ctx = d_contexts;
+  grouped_rows(wr, row_group, n_rows, t_ctx);
+  forecast_window(m, wr, d_out);
+  API_END
+}
+
+int t0h_forecast_grouped_ar(t0h_model* m, const float* contexts, const int64_t* row_group, size_t n_rows,
+                            size_t t_ctx, size_t horizon, size_t steps, float* out, size_t out_len) {
+  API_BEGIN
+  require(m && contexts && row_group && out, "t0h_forecast_grouped_ar: NULL argument");
+  require(n_rows > 0 && t_ctx > 0 && horizon > 0, "t0h_forecast_grouped_ar: sizes must be positive");
+  bind_device(m);
+  const size_t nq = m->mc.c.n_quantiles;
+  check_out(out_len, n_rows * steps * horizon * nq);
+  if (steps == 0) return T0H_OK;
+  const int qi = median_index(m->mc.c);
+  float* ctx_a = put(m, "ar_ctx_a", contexts, n_rows * t_ctx);
+  float* ctx_b = ws_get<float>(m, "ar_ctx_b", n_rows * t_ctx);
+  float* step_out = ws_get<float>(m, "ar_step", n_rows * horizon * nq);
+  float* result = ws_get<float>(m, "ar_out", n_rows * steps * horizon * nq);
+  for (size_t st = 0; st < steps; ++st) {
+    WindowRows wr;
+    wr.t_ctx = (int)t_ctx;
+    wr.horizon = (int)horizon;
+    wr.d_ctx = ctx_a;
+    grouped_rows(wr, row_group, n_rows, t_ctx);
+    forecast_window(m, wr, step_out);
+    launch_ar_store(result, step_out, (int)n_rows, (int)horizon, (int)nq, (int)steps, (int)st, m->stream);
+    launch_ar_shift(ctx_b, ctx_a, step_out, (int)n_rows, (int)t_ctx, (int)horizon, (int)nq, qi, m->stream);
+    std::swap(ctx_a, ctx_b);
+  }
+  download(m, out, result, n_rows * steps * horizon * nq);
+  sync(m);
+  API_END
+}
+
+int t0h_forecast_rollout(t0h_model* m, const float* context, size_t t_ctx, size_t prediction_length,
+                         const float* query, size_t n_query, float* out, size_t out_len) {
+  API_BEGIN
+  require(m && context && query && out, "t0h_forecast_rollout: NULL argument");
+  require(t_ctx > 0 && n_query > 0, "t0h_forecast_rollout: t_ctx and n_query must be positive");
+  bind_device(m);
+  check_out(out_len, prediction_length * n_query);
+  // model.rs:582-665 / lib.rs:259-341
+  const t0h_config& c = m->mc.c;
+  const size_t ps = c.patch_size, nt = c.n_quantiles;
+  const std::vector<float> q(query, query + n_query);
+  const std::vector<float> trained_mass = prob_mass(c.quantile_levels, nt);
+  const std::vector<float> query_mass = prob_mass(query, n_query);
+  const size_t context_width = (t_ctx + ps - 1) / ps * ps;
+  const size_t horizon0 = std::min<size_t>((prediction_length + ps - 1) / ps * ps, T0H_MAX_HORIZON);
+  std::vector<float> block0(horizon0 * nt);
+  forecast_host(m, context, 1, t_ctx, horizon0, block0.data());
+  std::vector<float> first;
+  for (size_t h = 0; h < horizon0; ++h) {
+    auto r = interpolate_quantiles(q, c.quantile_levels, block0.data() + h * nt, nt);
+    first.insert(first.end(), r.begin(), r.end());
+  }
+  std::vector<float> all(first);
+  if (prediction_length > horizon0) {
+    const size_t n_paths = n_query;
+    std::vector<std::vector<float>> paths(n_paths, std::vector<float>(context, context + t_ctx));
+    size_t remaining = prediction_length - horizon0;
+    std::vector<float> prev = first;
+    size_t prev_width = horizon0;
+    std::vector<float> weights(n_paths * nt), samples(n_paths * nt);
+    for (size_t j = 0; j < n_paths; ++j)
+      for (size_t pq = 0; pq < nt; ++pq) weights[j * nt + pq] = trained_mass[pq] * query_mass[j];
+    while (remaining > 0) {
+      for (size_t j = 0; j < n_paths; ++j)
+        for (size_t h = 0; h < prev_width; ++h) paths[j].push_back(prev[h * n_query + j]);
+      const size_t horizon = std::min<size_t>((remaining + ps - 1) / ps * ps, T0H_MAX_HORIZON);
+      std::vector<float> bctx(n_paths * context_width, 0.0f);
+      for (size_t j = 0; j < n_paths; ++j) {
+        const size_t wl = std::min(context_width, paths[j].size());
+        std::copy(paths[j].end() - wl, paths[j].end(), bctx.begin() + j * context_width + (context_width - wl));
+        // keep only what a future window can reach
+        if (paths[j].size() > 4 * context_width) paths[j].erase(paths[j].begin(), paths[j].end() - context_width);
+      }
+      std::vector<float> blocks(n_paths * horizon * nt);
+      forecast_batch_host(m, bctx.data(), n_paths, context_width, horizon, n_paths, blocks.data());
+      std::vector<float> reduced;
+      for (size_t h = 0; h < horizon; ++h) {
+        for (size_t j = 0; j < n_paths; ++j)
+          for (size_t pq = 0; pq < nt; ++pq) samples[j * nt + pq] = blocks[j * horizon * nt + h * nt + pq];
+        auto r = weighted_quantile(q, weights, samples);
+        reduced.insert(reduced.end(), r.begin(), r.end());
+      }
+      all.insert(all.end(), reduced.begin(), reduced.end());
+      prev = reduced;
+      prev_width = horizon;
+      remaining = remaining > horizon ? remaining - horizon : 0;  // saturating_sub (model.rs:660)
+    }
+  }
+  std::copy(all.begin(), all.begin() + prediction_length * n_query, out);
+  API_END
+}
+
+int t0h_dequant(int qtype, const void* d_blocks, size_t n, float* d_out, void* stream) {
+  API_BEGIN
+  launch_dequant(qtype, d_blocks, n, d_out, static_cast<hipStream_t>(stream));
+  API_END
+}
+
+int t0h_gemm_q(int wtype, const void* d_w, const float* d_x, const float* d_bias, float* d_y, size_t m, size_t n,
+               size_t k, int act, void* stream) {
+  API_BEGIN
+  require(m < (1u << 31) && n < (1u << 31) && k < (1u << 31), "t0h_gemm_q: dimension too large");
+  GemmDesc d;
+  d.wtype = wtype;
+  d.w = d_w;
+  d.a = d_x;
+  d.a_f32 = 1;
+  d.lda = (int)k;
+  d.bias = d_bias;
+  d.y = d_y;
+  d.ldy = (int)n;
+  d.M = (int)m;
+  d.N = (int)n;
+  d.K = (int)k;
+  d.relu = act == 1;
+  d.epi = EPI_STORE_F32;
+  launch_gemm(d, static_cast<hipStream_t>(stream));
+  API_END
+}
+
+size_t t0h_row_bytes(int qtype, size_t n) { return row_bytes(qtype, n); }
+
+int t0h_quantize(int qtype, const float* x, size_t n, uint8_t* out, size_t out_len) {
+  API_BEGIN
+  const size_t nb = row_bytes(qtype, n);
+  if (nb == 0 && n != 0) throw Error(T0H_ERR_SHAPE, "quantize: element count is not a multiple of 32");
+  require(out_len >= nb, "quantize: output buffer too small");
+  require((x && out) || n == 0, "quantize: NULL argument");
+  quantize(qtype, x, n, out);
+  API_END
+}
+
+int t0h_synth_model_gguf(const t0h_synth_spec* spec, int quant, uint8_t* out, size_t cap, size_t* len) {
+  API_BEGIN
+  require(spec && len, "t0h_synth_model_gguf: NULL argument");
+  std::vector<uint8_t> b = synth_model_gguf(*spec, quant);
+  *len = b.size();
+  if (out) {
+    require(cap >= b.size(), "t0h_synth_model_gguf: output buffer too small");
+    std::memcpy(out, b.data(), b.size());
+  }
+  API_END
+}
+
+int t0h_export_gguf(const uint8_t* bytes, size_t len, int quant, uint8_t* out, size_t cap, size_t* out_len) {
+  API_BEGIN
+  require(bytes && out_len, "t0h_export_gguf: NULL argument");
+  std::vector<uint8_t> b = export_gguf(bytes, len, quant);
+  *out_len = b.size();
+  if (out) {
+    require(cap >= b.size(), "t0h_export_gguf: output buffer too small");
+    std::memcpy(out, b.data(), b.size());
+  }
+  API_END
+}
+
+}  // extern "C"
