@@ -1,0 +1,249 @@
+#!/usr/bin/env python3
+"""Throughput benchmark of the t0hip quantized-inference path on one MI355X.
+
+Step = one batched forecast of BASELINE config 4: 256 series x 3 variates, each
+with a 2048-step context (sine mixture x lognormal scale, 10% NaN gaps in runs
+of 16-128), horizon 64, through the 12-layer / embed 768 synthetic t0 model
+with Q4_0 weights (random init from a fixed seed).  Inputs are resident in HBM
+(t0h_forecast_grouped_dev); `value` is series forecasts per second.
+
+Also reported on the same JSON line:
+  roofline      the dominant kernel of the step (by total time), timed with HIP
+                events on the model's stream inside the real forward;
+  cpu_baseline  the oracle (this repo's C restatement of t0-core's ndarray path,
+                f32 dequant-at-load + OpenMP GEMM) on a bounded sample of the
+                same workload on this host's cores;
+  gemm_sweep    BASELINE configs 1-2: the kernel-level Q-GEMM (f32 in/out) at
+                M in {1,16,64,512,8192} x (K,N) shapes, TFLOP/s and GB/s;
+                small-M cases rotate through >256 MB of weight copies so the
+                Infinity Cache cannot serve them.
+"""
+import argparse
+import json
+import os
+import sys
+import time
+
+import numpy as np
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, os.path.join(ROOT, "t0-web_amd"))
+
+HBM_PEAK_GBS = 8000.0
+MFMA_F16_PEAK_TFLOPS = 2500.0
+METRIC = "Q-GEMM TFLOPS & HBM GB/s vs roofline; forecasts/sec at 256 series on 1 GPU"
+
+
+def log(msg):
+    print(f"[bench] {msg}", file=sys.stderr, flush=True)
+
+
+def config4_inputs(n_series=256, n_var=3, t_ctx=2048, seed=0):
+    """Sine mixture x lognormal scale per series, 10% NaN gaps in contiguous runs of 16..128."""
+    rng = np.random.default_rng(seed)
+    rows = n_series * n_var
+    tt = np.arange(t_ctx, dtype=np.float64)
+    x = np.zeros((rows, t_ctx))
+    for _ in range(3):
+        period = rng.uniform(7, 365, (rows, 1))
+        phase = rng.uniform(0, 2 * np.pi, (rows, 1))
+        x += rng.uniform(0.5, 2.0, (rows, 1)) * np.sin(2 * np.pi * tt / period + phase)
+    x += 0.1 * rng.standard_normal((rows, t_ctx))
+    x *= np.repeat(np.exp(rng.standard_normal(n_series)), n_var)[:, None]
+    for r in range(rows):
+        while np.isnan(x[r]).sum() < 0.1 * t_ctx:
+            L = int(rng.integers(16, 129))
+            s = int(rng.integers(0, t_ctx - L))
+            x[r, s:s + L] = np.nan
+    groups = np.repeat(np.arange(n_series), n_var).astype(np.int64)
+    return x.astype(np.float32), groups
+
+
+def gemm_flops(name, M, cfg):
+    E, H = cfg.embed_dim, cfg.mlp_hidden_dim
+    return {"gemm_w0_swiglu": 2 * M * 2 * H * E, "gemm_qkv": 2 * M * 3 * E * E,
+            "gemm_w2_resid": 2 * M * E * H, "gemm_wo_resid": 2 * M * E * E}.get(name)
+
+
+def gemm_bytes(name, M, cfg, wbytes_per_val):
+    """Algorithmic HBM bytes of one launch: weight blocks + f16 activations in + outputs."""
+    E, H = cfg.embed_dim, cfg.mlp_hidden_dim
+    if name == "gemm_w0_swiglu":
+        return 2 * H * E * wbytes_per_val + M * E * 2 + M * H * 2 + 2 * H * 4
+    if name == "gemm_qkv":
+        return 3 * E * E * wbytes_per_val + M * E * 2 + M * 3 * E * 2 + 3 * E * 4
+    if name == "gemm_w2_resid":
+        return E * H * wbytes_per_val + M * H * 2 + 2 * M * E * 4 + E * 4
+    if name == "gemm_wo_resid":
+        return E * E * wbytes_per_val + M * E * 2 + 2 * M * E * 4 + E * 4
+    return None
+
+
+def gemm_sweep(torch, t0hip, iters=20):
+    """BASELINE configs 1-2 through the kernel-level t0h_gemm_q (f32 x in, f32 y out)."""
+    rng = np.random.default_rng(7)
+    stream = torch.cuda.current_stream()
+    out = []
+    shapes = [(768, 2304), (768, 768), (768, 2048), (2048, 768), (768, 4096)]
+    for qtype, qname, bpv in ((t0hip.Q8_0, "q8_0", 34 / 32), (t0hip.Q4_0, "q4_0", 18 / 32)):
+        for K, N in shapes:
+            W = (0.02 * rng.standard_normal((N, K))).astype(np.float32)
+            blocks = t0hip.quantize(qtype, W)
+            for M in (1, 16, 64, 512, 8192):
+                # rotate weight copies past the 256 MB Infinity Cache for the bandwidth-bound cases
+                n_copies = max(1, int(np.ceil(320e6 / blocks.size))) if M <= 64 else 1
+                dW = torch.from_numpy(blocks).cuda().repeat(n_copies)
+                x = torch.randn((M, K), dtype=torch.float32, device="cuda")
+                y = torch.empty((M, N), dtype=torch.float32, device="cuda")
+                stride = blocks.size
+
+                def run(i):
+                    t0hip.gemm_q_dev(qtype, dW.data_ptr() + (i % n_copies) * stride, x.data_ptr(), 0, y.data_ptr(),
+                                     M, N, K, 0, stream.cuda_stream)
+
+                for i in range(3):
+                    run(i)
+                reps = max(iters, n_copies)
+                e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+                e0.record(stream)
+                for i in range(reps):
+                    run(i)
+                e1.record(stream)
+                torch.cuda.synchronize()
+                us = e0.elapsed_time(e1) * 1e3 / reps
+                flops = 2.0 * M * N * K
+                nbytes = N * K * bpv + M * K * 4 + M * N * 4
+                tflops = flops / us * 1e-6
+                gbs = nbytes / us * 1e-3
+                ai = flops / nbytes
+                bound = "mfma" if ai * HBM_PEAK_GBS * 1e9 > MFMA_F16_PEAK_TFLOPS * 1e12 else "hbm"
+                frac = tflops / MFMA_F16_PEAK_TFLOPS if bound == "mfma" else gbs / HBM_PEAK_GBS
+                out.append({"quant": qname, "M": M, "K": K, "N": N, "us": round(us, 2), "tflops": round(tflops, 2),
+                            "gbs": round(gbs, 1), "bound": bound, "frac": round(frac, 3)})
+                del dW, x, y
+    return out
+
+
+def cpu_baseline(gguf, x, groups, t_ctx, horizon, budget_s=12.0):
+    """Oracle forecast on a bounded sample of the same workload (whole series, 3 variates each)."""
+    sys.path.insert(0, os.path.join(ROOT, "oracle"))
+    import t0ref  # the CPU checker/baseline, test infrastructure
+
+    threads = int(os.environ.get("OMP_NUM_THREADS", "0")) or (os.cpu_count() or 1)
+    t0ref.set_threads(threads)
+    om = t0ref.Model(gguf)
+    n_var = 3
+    n = 2
+    t = time.perf_counter()
+    om.forecast_grouped(x[: n * n_var], groups[: n * n_var], t_ctx, horizon)
+    first = time.perf_counter() - t
+    n = max(1, min(64, int(budget_s / max(first / 2, 1e-3))))
+    t = time.perf_counter()
+    om.forecast_grouped(x[: n * n_var], groups[: n * n_var], t_ctx, horizon)
+    dt = time.perf_counter() - t
+    return {"value": round(n / dt, 3), "unit": "forecasts/s", "cores": threads, "kind": "port",
+            "sample": f"{n} series x {n_var} variates (of 256), ctx {t_ctx}, h {horizon}, one forecast_grouped call, "
+                      f"{dt:.1f} s"}
+
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=20)
+    ap.add_argument("--warmup", type=int, default=3)
+    ap.add_argument("--profile-steps", type=int, default=5)
+    ap.add_argument("--no-sweep", action="store_true")
+    ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--quant", default="q4_0", choices=["q4_0", "q8_0"])
+    args = ap.parse_args()
+    world = int(os.environ.get("WORLD_SIZE", "1"))
+    if args.gpus != 1 or world != 1:
+        print("bench.py measures one GPU only: this build runs the whole forecast on a single MI355X "
+              "(series shard across GPUs with no collectives; see DESIGN.md). Use --gpus 1.", file=sys.stderr)
+        sys.exit(2)
+
+    import torch
+    import t0hip
+
+    qtype = t0hip.Q4_0 if args.quant == "q4_0" else t0hip.Q8_0
+    bpv = 18 / 32 if args.quant == "q4_0" else 34 / 32
+    cfg = t0hip.make_config()  # 12 layers, embed 768, 12 heads, hidden 2048, patch 32, 9 quantiles
+    log("synthesizing model")
+    gguf = t0hip.synth_model_gguf(cfg, quant=qtype, seed=0)
+    engine = t0hip.Engine(0)
+    model = t0hip.load_model_from_gguf(engine, gguf)
+    n_series, n_var, t_ctx, horizon = 256, 3, 2048, 64
+    x, groups = config4_inputs(n_series, n_var, t_ctx)
+    d_x = torch.from_numpy(x).cuda()
+    d_out = torch.empty((n_series * n_var, horizon, cfg.n_quantiles), dtype=torch.float32, device="cuda")
+
+    def step():
+        t0hip.forecast_grouped_dev(model, d_x.data_ptr(), groups, t_ctx, horizon, d_out.data_ptr())
+
+    log(f"warmup {args.warmup}")
+    for _ in range(args.warmup):
+        step()
+    torch.cuda.synchronize()
+    log(f"timing {args.steps} steps")
+    t0 = time.perf_counter()
+    for _ in range(args.steps):
+        step()
+    torch.cuda.synchronize()
+    elapsed = time.perf_counter() - t0
+    ms_per_step = elapsed / args.steps * 1e3
+    value = n_series * args.steps / elapsed
+    log(f"{ms_per_step:.3f} ms/step, {value:.1f} forecasts/s")
+
+    # per-kernel-kind event timing inside the real forward
+    model.profile(True)
+    for _ in range(args.profile_steps):
+        step()
+    torch.cuda.synchronize()
+    prof = model.profile_report()
+    model.profile(False)
+    M = n_series * n_var * ((t_ctx + horizon + 31) // 32)
+    kernels = {k: {"launches": n, "avg_us": round(ms / max(n, 1) * 1e3, 2), "total_ms_per_step": round(ms / args.profile_steps, 3)}
+               for k, (n, ms) in prof.items()}
+    gemm_names = [k for k in prof if gemm_flops(k, M, cfg)]
+    dom = max(gemm_names, key=lambda k: prof[k][1])
+    n_l, ms_l = prof[dom]
+    avg_s = ms_l / n_l * 1e-3
+    flops = gemm_flops(dom, M, cfg)
+    achieved = flops / avg_s * 1e-12
+    roofline = {"kernel": dom, "bound": "mfma", "achieved": round(achieved, 1), "peak": MFMA_F16_PEAK_TFLOPS,
+                "unit": "TFLOP/s", "frac": round(achieved / MFMA_F16_PEAK_TFLOPS, 4), "traffic": None,
+                "flops_per_launch": flops, "algorithmic_bytes_per_launch": int(gemm_bytes(dom, M, cfg, bpv)),
+                "avg_launch_us": round(avg_s * 1e6, 2)}
+    total_gemm_flops = sum(gemm_flops(k, M, cfg) * prof[k][0] for k in gemm_names) / args.profile_steps
+    total_gemm_ms = sum(prof[k][1] for k in gemm_names) / args.profile_steps
+    log(f"dominant kernel {dom}: {roofline['avg_launch_us']} us, {achieved:.0f} TFLOP/s")
+
+    sweep = None
+    if not args.no_sweep:
+        log("GEMM sweep (configs 1-2)")
+        sweep = gemm_sweep(torch, t0hip)
+    cpu = None
+    if not args.no_cpu:
+        log("CPU baseline (oracle)")
+        cpu = cpu_baseline(gguf, x, groups, t_ctx, horizon)
+        log(f"cpu {cpu['value']} forecasts/s on {cpu['cores']} threads")
+
+    line = {
+        "metric": METRIC, "value": round(value, 2), "unit": "forecasts/s", "n_gpus": 1, "steps": args.steps,
+        "warmup": args.warmup, "ms_per_step": round(ms_per_step, 3), "higher_is_better": True, "scaling": "weak",
+        "vs_baseline": None, "dtype": "f16", "data": "synthetic",
+        "config": {"workload": "BASELINE config 4: 256 series x 3 variates, ctx 2048, horizon 64, "
+                               f"{args.quant.upper()} synthetic t0 (12 layers, embed 768, 12 heads, SwiGLU 2048, "
+                               "9 quantiles), sine mixture x lognormal scale, 10% NaN gaps",
+                   "rows": n_series * n_var, "patches": M // (n_series * n_var), "gemm_rows": M},
+        "roofline": roofline,
+        "cpu_baseline": cpu,
+        "forward_gemm_tflops": round(total_gemm_flops / (total_gemm_ms * 1e-3) * 1e-12, 1),
+        "kernels": kernels,
+        "gemm_sweep": sweep,
+    }
+    print(json.dumps(line), flush=True)
+
+
+if __name__ == "__main__":
+    main()

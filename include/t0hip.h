@@ -115,6 +115,15 @@ void* t0h_model_stream(const t0h_model* model);
  * number of device allocations made since load (≡ Pool::alloc_count, pool.rs:51-57). */
 int t0h_model_workspace(const t0h_model* model, uint64_t* resident_bytes, uint64_t* alloc_count);
 
+/* Per-kernel-kind timing of this model's forward with HIP events on its stream
+ * (no counterpart in the reference, which has no tracer: engine.rs:186-189 sets
+ * timestamp_writes: None).  enable = 1 resets the counters and starts
+ * recording; 0 stops.  Entries are indexed 0..n-1 in first-seen order; an index
+ * past the end returns T0H_ERR_INVALID_ARG. */
+int t0h_model_profile(t0h_model* model, int enable);
+int t0h_model_profile_entry(t0h_model* model, size_t i, char* name, size_t name_cap, uint64_t* launches,
+                            double* total_ms);
+
 /* ---- forward ----------------------------------------------------------- */
 /* ≡ model::forward_async (t0-fast model.rs:693-808) ≡ T0Model::forward (t0-core
  * model.rs:159-244): `series` already padded to whole patches and scaled.

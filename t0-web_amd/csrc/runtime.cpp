@@ -9,6 +9,7 @@
 
 #include <algorithm>
 #include <cmath>
+#include <cstdio>
 #include <cstring>
 #include <memory>
 #include <numeric>
@@ -74,6 +75,20 @@ struct Workspace {
   int rope_p = -1;
 };
 
+// Per-kernel-kind timing with HIP events recorded on the model's stream around
+// each launch of the forward (enabled on demand; off by default).
+struct ProfEntry {
+  std::string name;
+  std::vector<std::pair<hipEvent_t, hipEvent_t>> pending;
+  uint64_t launches = 0;
+  double total_ms = 0.0;
+};
+struct Profiler {
+  bool on = false;
+  std::vector<ProfEntry> entries;
+  std::vector<hipEvent_t> spare;
+};
+
 }  // namespace t0h
 
 struct t0h_ctx {
@@ -94,6 +109,7 @@ struct t0h_model {
   const float* out_norm = nullptr;
   std::vector<t0h::Layer> layers;
   t0h::Workspace ws;
+  t0h::Profiler prof;
 };
 
 namespace t0h {
@@ -157,6 +173,60 @@ void download(t0h_model* m, T* dst, const T* src, size_t n) {
   if (n) hip_check(hipMemcpyAsync(dst, src, n * sizeof(T), hipMemcpyDeviceToHost, m->stream), "hipMemcpyAsync D2H");
 }
 void sync(t0h_model* m) { hip_check(hipStreamSynchronize(m->stream), "hipStreamSynchronize"); }
+
+hipEvent_t prof_event(t0h_model* m) {
+  if (!m->prof.spare.empty()) {
+    hipEvent_t e = m->prof.spare.back();
+    m->prof.spare.pop_back();
+    return e;
+  }
+  hipEvent_t e;
+  hip_check(hipEventCreate(&e), "hipEventCreate");
+  return e;
+}
+
+// Scope guard: times the launches issued inside it under `name`.
+struct ProfScope {
+  t0h_model* m;
+  size_t idx = 0;
+  hipEvent_t start = nullptr;
+  ProfScope(t0h_model* model, const char* name) : m(model) {
+    if (!m->prof.on) return;
+    auto& es = m->prof.entries;
+    idx = es.size();
+    for (size_t i = 0; i < es.size(); ++i)
+      if (es[i].name == name) idx = i;
+    if (idx == es.size()) {
+      es.emplace_back();
+      es.back().name = name;
+    }
+    start = prof_event(m);
+    hip_check(hipEventRecord(start, m->stream), "hipEventRecord");
+  }
+  ~ProfScope() {
+    if (!start) return;
+    hipEvent_t end = prof_event(m);
+    if (hipEventRecord(end, m->stream) == hipSuccess) m->prof.entries[idx].pending.emplace_back(start, end);
+  }
+};
+
+void prof_collect(t0h_model* m) {
+  bool any = false;
+  for (auto& e : m->prof.entries) any |= !e.pending.empty();
+  if (!any) return;
+  sync(m);
+  for (auto& e : m->prof.entries) {
+    for (auto& pr : e.pending) {
+      float ms = 0.0f;
+      hip_check(hipEventElapsedTime(&ms, pr.first, pr.second), "hipEventElapsedTime");
+      e.total_ms += ms;
+      e.launches++;
+      m->prof.spare.push_back(pr.first);
+      m->prof.spare.push_back(pr.second);
+    }
+    e.pending.clear();
+  }
+}
 
 // ---- load ----
 size_t align256(size_t x) { return (x + 255) & ~size_t(255); }
@@ -408,12 +478,15 @@ void encode_and_layers(t0h_model* m, int v, int p, const PatchMeta& pm, float* t
   ensure_rope(m, p);
 
   // patch encoder residual block + type embedding (model.rs:199-207)
-  launch_gemm(gemm(m->enc.hid, pm.enc_in, 3 * ps, m->enc.hb, xn, m->enc.hid.n, M, EPI_STORE_F16, 1), s);
-  GemmDesc rd = gemm(m->enc.res, pm.enc_in, 3 * ps, m->enc.rb, x, E, M, EPI_STORE_F32);
-  rd.row_add = m->type_emb;
-  rd.row_add_idx = pm.type_idx;
-  launch_gemm(rd, s);
-  launch_gemm(gemm(m->enc.out, xn, m->enc.hid.n, m->enc.ob, x, E, M, EPI_RESID_F32), s);
+  {
+    ProfScope ps_(m, "gemm_encoder");
+    launch_gemm(gemm(m->enc.hid, pm.enc_in, 3 * ps, m->enc.hb, xn, m->enc.hid.n, M, EPI_STORE_F16, 1), s);
+    GemmDesc rd = gemm(m->enc.res, pm.enc_in, 3 * ps, m->enc.rb, x, E, M, EPI_STORE_F32);
+    rd.row_add = m->type_emb;
+    rd.row_add_idx = pm.type_idx;
+    launch_gemm(rd, s);
+    launch_gemm(gemm(m->enc.out, xn, m->enc.hid.n, m->enc.ob, x, E, M, EPI_RESID_F32), s);
+  }
   if (trace_pe) download(m, trace_pe, x, (size_t)M * E);
 
   AttnDesc ad;
@@ -434,18 +507,39 @@ void encode_and_layers(t0h_model* m, int v, int p, const PatchMeta& pm, float* t
   ad.seg_len = seg_len;
   for (size_t li = 0; li < m->layers.size(); ++li) {
     const Layer& L = m->layers[li];
-    launch_rmsnorm(x, L.norm, xn, nullptr, M, E, s);
-    launch_gemm(gemm(L.qkv, xn, E, L.b_qkv, qkv, 3 * E, M, EPI_STORE_F16), s);
+    {
+      ProfScope ps_(m, "rmsnorm");
+      launch_rmsnorm(x, L.norm, xn, nullptr, M, E, s);
+    }
+    {
+      ProfScope ps_(m, "gemm_qkv");
+      launch_gemm(gemm(L.qkv, xn, E, L.b_qkv, qkv, 3 * E, M, EPI_STORE_F16), s);
+    }
     ad.q_norm = L.q_norm;
     ad.k_norm = L.k_norm;
-    if (L.group)
+    if (L.group) {
+      ProfScope ps_(m, "attn_group");
       launch_group_attention(ad, s);
-    else
+    } else {
+      ProfScope ps_(m, "attn_time");
       launch_time_attention(ad, s);
-    launch_gemm(gemm(L.o, xn, E, L.b_o, x, E, M, EPI_RESID_F32), s);
-    launch_rmsnorm(x, L.mlp_norm, xn, nullptr, M, E, s);
-    launch_gemm(gemm(L.w0, xn, E, L.b0, hb, H, M, EPI_SWIGLU_F16), s);
-    launch_gemm(gemm(L.w2, hb, H, L.b2, x, E, M, EPI_RESID_F32), s);
+    }
+    {
+      ProfScope ps_(m, "gemm_wo_resid");
+      launch_gemm(gemm(L.o, xn, E, L.b_o, x, E, M, EPI_RESID_F32), s);
+    }
+    {
+      ProfScope ps_(m, "rmsnorm");
+      launch_rmsnorm(x, L.mlp_norm, xn, nullptr, M, E, s);
+    }
+    {
+      ProfScope ps_(m, "gemm_w0_swiglu");
+      launch_gemm(gemm(L.w0, xn, E, L.b0, hb, H, M, EPI_SWIGLU_F16), s);
+    }
+    {
+      ProfScope ps_(m, "gemm_w2_resid");
+      launch_gemm(gemm(L.w2, hb, H, L.b2, x, E, M, EPI_RESID_F32), s);
+    }
     if (li == 0 && trace_l0) download(m, trace_l0, x, (size_t)M * E);
   }
 }
@@ -459,6 +553,7 @@ float* decode_rows(t0h_model* m, int rows, const int* map) {
   _Float16* din = ws_get<_Float16>(m, "dec_in", (size_t)rows * E);
   _Float16* dh = ws_get<_Float16>(m, "dec_h", (size_t)rows * m->dec.hid.n);
   float* dout = ws_get<float>(m, "dec_out", (size_t)rows * nout);
+  ProfScope ps_(m, "decoder");
   launch_rmsnorm(x, m->out_norm, din, map, rows, E, s);
   launch_gemm(gemm(m->dec.hid, din, E, m->dec.hb, dh, m->dec.hid.n, rows, EPI_STORE_F16, 1), s);
   launch_gemm(gemm(m->dec.res, din, E, m->dec.rb, dout, nout, rows, EPI_STORE_F32), s);
@@ -523,15 +618,22 @@ void forecast_window(t0h_model* m, const WindowRows& wr, float* d_out) {
   float* loc = ws_get<float>(m, "loc", (size_t)v * t);
   float* scl = ws_get<float>(m, "scale", (size_t)v * t);
   PatchMeta pm = patch_buffers(m, v, p);
-  launch_window_welford(w, loc, scl, s);
-  PatchOut po{pm.enc_in, pm.grp, pm.att, pm.type_idx, pm.type_raw, pm.fut, pm.patch_loc, pm.patch_scale};
-  launch_window_patchify(w, loc, scl, po, s);
-  launch_fut_rows(pm.type_raw, pm.fut, v, p, s);
+  {
+    ProfScope ps_(m, "prep_welford");
+    launch_window_welford(w, loc, scl, s);
+  }
+  {
+    ProfScope ps_(m, "prep_patchify");
+    PatchOut po{pm.enc_in, pm.grp, pm.att, pm.type_idx, pm.type_raw, pm.fut, pm.patch_loc, pm.patch_scale};
+    launch_window_patchify(w, loc, scl, po, s);
+    launch_fut_rows(pm.type_raw, pm.fut, v, p, s);
+  }
   encode_and_layers(m, v, p, pm, nullptr, nullptr);
   if (hp == 0) return;
   int* map = ws_get<int>(m, "dec_map", (size_t)v * hp);
   launch_gather_map(map, v, p, ctx_p, hp, s);
   float* dout = decode_rows(m, v * hp, map);
+  ProfScope ps_(m, "forecast_out");
   ForecastOutDesc od;
   od.dec = dout;
   od.patch_loc = pm.patch_loc;
@@ -765,6 +867,12 @@ void t0h_model_destroy(t0h_model* m) {
     if (kv.second.p) (void)hipHostFree(kv.second.p);
     if (kv.second.ev) (void)hipEventDestroy(kv.second.ev);
   }
+  for (auto& e : m->prof.entries)
+    for (auto& pr : e.pending) {
+      (void)hipEventDestroy(pr.first);
+      (void)hipEventDestroy(pr.second);
+    }
+  for (hipEvent_t e : m->prof.spare) (void)hipEventDestroy(e);
   if (m->d_weights) (void)hipFree(m->d_weights);
   (void)hipStreamDestroy(m->stream);
   delete m;
@@ -795,6 +903,35 @@ int t0h_model_workspace(const t0h_model* m, uint64_t* resident, uint64_t* allocs
   for (const auto& kv : m->ws.bufs) b += kv.second.cap;
   if (resident) *resident = b;
   if (allocs) *allocs = m->ws.allocs;
+  API_END
+}
+
+int t0h_model_profile(t0h_model* m, int enable) {
+  API_BEGIN
+  require(m != nullptr, "t0h_model_profile: NULL model");
+  bind_device(m);
+  prof_collect(m);
+  for (auto& e : m->prof.entries) {
+    e.launches = 0;
+    e.total_ms = 0.0;
+  }
+  m->prof.on = enable != 0;
+  API_END
+}
+
+int t0h_model_profile_entry(t0h_model* m, size_t i, char* name, size_t name_cap, uint64_t* launches,
+                            double* total_ms) {
+  API_BEGIN
+  require(m != nullptr, "t0h_model_profile_entry: NULL model");
+  bind_device(m);
+  prof_collect(m);
+  if (i >= m->prof.entries.size()) throw Error(T0H_ERR_INVALID_ARG, "profile entry index out of range");
+  const ProfEntry& e = m->prof.entries[i];
+  if (name && name_cap) {
+    std::snprintf(name, name_cap, "%s", e.name.c_str());
+  }
+  if (launches) *launches = e.launches;
+  if (total_ms) *total_ms = e.total_ms;
   API_END
 }
 

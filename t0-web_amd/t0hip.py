@@ -73,7 +73,7 @@ _lib = None
 SYMBOLS = [
     "t0h_last_error", "t0h_abi_version", "t0h_ctx_create", "t0h_ctx_destroy", "t0h_gguf_inspect",
     "t0h_model_load_gguf", "t0h_model_destroy", "t0h_model_config", "t0h_model_weight_bytes", "t0h_model_stream",
-    "t0h_model_workspace", "t0h_forward", "t0h_forecast", "t0h_forecast_batch_chunked",
+    "t0h_model_workspace", "t0h_model_profile", "t0h_model_profile_entry", "t0h_forward", "t0h_forecast", "t0h_forecast_batch_chunked",
     "t0h_forecast_batch_rows_chunked", "t0h_forecast_grouped", "t0h_forecast_grouped_dev",
     "t0h_forecast_grouped_ar", "t0h_forecast_rollout", "t0h_dequant", "t0h_gemm_q", "t0h_row_bytes",
     "t0h_quantize", "t0h_synth_model_gguf", "t0h_export_gguf",
@@ -104,6 +104,8 @@ def lib():
     L.t0h_model_stream.restype = P
     L.t0h_model_stream.argtypes = [P]
     L.t0h_model_workspace.argtypes = [P, C.POINTER(C.c_uint64), C.POINTER(C.c_uint64)]
+    L.t0h_model_profile.argtypes = [P, I]
+    L.t0h_model_profile_entry.argtypes = [P, S, C.c_char_p, S, C.POINTER(C.c_uint64), C.POINTER(C.c_double)]
     L.t0h_forward.argtypes = [P, C.POINTER(Series), P, S, P, P]
     L.t0h_forecast.argtypes = [P, P, S, S, S, P, S]
     L.t0h_forecast_batch_chunked.argtypes = [P, P, S, S, S, S, P, S]
@@ -256,6 +258,24 @@ class GpuModel:
         q, t = C.c_uint64(), C.c_uint64()
         _check(lib().t0h_model_weight_bytes(self.h, C.byref(q), C.byref(t)))
         return t.value
+
+    def profile(self, enable=True):
+        """Start (reset) or stop per-kernel-kind event timing of this model's forward."""
+        _check(lib().t0h_model_profile(self.h, int(enable)))
+
+    def profile_report(self):
+        """{kernel kind: (launches, total_ms)} recorded since profile(True)."""
+        out = {}
+        i = 0
+        name = C.create_string_buffer(128)
+        while True:
+            n, ms = C.c_uint64(), C.c_double()
+            rc = lib().t0h_model_profile_entry(self.h, i, name, 128, C.byref(n), C.byref(ms))
+            if rc != 0:
+                break
+            out[name.value.decode()] = (n.value, ms.value)
+            i += 1
+        return out
 
     def workspace(self):
         r, a = C.c_uint64(), C.c_uint64()
