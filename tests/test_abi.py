@@ -1,0 +1,62 @@
+"""The C ABI library (CPU): it loads without a GPU, exports every entry point
+include/t0hip.h declares, the Python binding binds exactly those, and the
+host-only entry points validate their arguments."""
+import ctypes as C
+import os
+import re
+
+import numpy as np
+import pytest
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+
+
+def declared():
+    src = open(os.path.join(ROOT, "include", "t0hip.h")).read()
+    src = re.sub(r"/\*.*?\*/", "", src, flags=re.S)
+    return sorted(set(re.findall(r"\b(t0h_[a-z0-9_]+)\s*\(", src)))
+
+
+def test_every_declared_symbol_is_exported(t0hip):
+    names = declared()
+    assert len(names) >= 25
+    L = C.CDLL(t0hip.LIB_PATH)
+    missing = [n for n in names if not hasattr(L, n)]
+    assert not missing, missing
+    assert sorted(t0hip.SYMBOLS) == names
+
+
+def test_abi_version_and_no_device(t0hip):
+    assert t0hip.lib().t0h_abi_version() == 1
+    import torch
+    if torch.cuda.is_available():
+        pytest.skip("a GPU is visible")
+    with pytest.raises(t0hip.T0HipError) as e:
+        t0hip.Engine(0)
+    assert e.value.status == "NO_DEVICE"
+
+
+def test_host_entry_points_validate(t0hip):
+    with pytest.raises(t0hip.T0HipError) as e:
+        t0hip.synth_model_gguf(t0hip.make_config(embed_dim=100, num_heads=3))
+    assert e.value.status == "INVALID_ARG"
+    with pytest.raises(t0hip.T0HipError) as e:
+        t0hip.export_gguf(b"not a gguf at all", 8)
+    assert e.value.status == "GGUF_MAGIC"
+    L = t0hip.lib()
+    assert L.t0h_gguf_inspect(None, 0, None, None) == -2  # empty input: bad magic
+    assert L.t0h_forecast(None, None, 1, 1, 1, None, 0) == -1
+    assert L.t0h_model_config(None, None) == -1
+    x = np.zeros(64, np.float32)
+    out = np.zeros(10, np.uint8)
+    assert L.t0h_quantize(8, x.ctypes.data_as(C.c_void_p), 64, out.ctypes.data_as(C.c_void_p), 10) == -1
+
+
+def test_no_cpu_fallback_in_product():
+    """The product package never imports or loads the oracle."""
+    pkg = os.path.join(ROOT, "t0-web_amd")
+    for dirpath, _, files in os.walk(pkg):
+        for f in files:
+            if f.endswith((".py", ".cpp", ".hip", ".h")):
+                text = open(os.path.join(dirpath, f), errors="ignore").read()
+                assert "t0ref" not in text and "libt0ref" not in text, f
