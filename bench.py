@@ -155,6 +155,8 @@ def main():
     ap.add_argument("--no-sweep", action="store_true")
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--quant", default="q4_0", choices=["q4_0", "q8_0"])
+    ap.add_argument("--calibrate-copy", action="store_true",
+                    help="first run one plain 256 MiB device-to-device copy (reference for PMC byte counters)")
     args = ap.parse_args()
     world = int(os.environ.get("WORLD_SIZE", "1"))
     if args.gpus != 1 or world != 1:
@@ -165,6 +167,12 @@ def main():
     import torch
     import t0hip
 
+    if args.calibrate_copy:
+        src = torch.empty(256 << 20, dtype=torch.uint8, device="cuda")
+        dst = torch.empty_like(src)
+        dst.copy_(src)
+        torch.cuda.synchronize()
+        del src, dst
     qtype = t0hip.Q4_0 if args.quant == "q4_0" else t0hip.Q8_0
     bpv = 18 / 32 if args.quant == "q4_0" else 34 / 32
     cfg = t0hip.make_config()  # 12 layers, embed 768, 12 heads, hidden 2048, patch 32, 9 quantiles

@@ -39,8 +39,12 @@ size_t time_attn_lds(int p) {
   return (size_t)(P16 + P32) * LDH * 2 + (size_t)HD * (P32 + 8) * 2 + (size_t)P32 * 4 + (size_t)P32;
 }
 
-// One workgroup per (variate row, head); 4 waves; MFMA 16x16x32 f16 for both
-// S^T = K Q^T and O = P V, scores of a 16-query tile kept in registers.
+// One workgroup per (variate row, head); 4 waves.  Load phase: 8 lanes per
+// 64-wide q/k/v row (16 B each), QK-RMSNorm reduced over the 8-lane group,
+// interleaved xPos RoPE on the lane's 4 adjacent pairs, q/k stored row-major
+// and v transposed into LDS.  Compute phase: per 16-query tile, S^T = K Q^T
+// and O = P V on v_mfma_f32_16x16x32_f16 with the tile's scores in registers.
+template <int MAXKT>
 __global__ __launch_bounds__(256) void k_time_attn(const AttnDesc d) {
   extern __shared__ __align__(16) _Float16 sm[];
   const int p = d.p, P16 = round_up(p, 16), P32 = round_up(p, 32), LDV = P32 + 8;
@@ -59,60 +63,53 @@ __global__ __launch_bounds__(256) void k_time_attn(const AttnDesc d) {
     Gk[i] = i < p ? d.grp[row0 + i] : -2;
     Ak[i] = i < p ? d.att[row0 + i] : 0;
   }
-  // load q, k (normalized + rotated) and v (transposed) for this head
-  for (int task = tid; task < 3 * P32; task += 256) {
-    const int which = task / P32, i = task % P32;
-    if (which == 0 && i >= P16) continue;
-    if (i >= p) {
-      if (which < 2) {
-        uint4* dst = reinterpret_cast<uint4*>((which ? Ks : Qs) + i * LDH);
-#pragma unroll
-        for (int c = 0; c < 8; ++c) dst[c] = make_uint4(0, 0, 0, 0);
-      } else {
-        for (int dd = 0; dd < HD; ++dd) Vt[dd * LDV + i] = (_Float16)0.0f;
-      }
-      continue;
+  const int n_items = P16 + 2 * P32;
+  const int d0 = (tid & 7) * 8;
+  for (int item = tid >> 3; item < n_items; item += 32) {
+    int which, i;
+    if (item < P16) {
+      which = 0;
+      i = item;
+    } else if (item < P16 + P32) {
+      which = 1;
+      i = item - P16;
+    } else {
+      which = 2;
+      i = item - P16 - P32;
     }
-    const uint4* src = reinterpret_cast<const uint4*>(d.qkv + (row0 + i) * ld + (size_t)which * E + h * HD);
-    _Float16 xh[HD];
-#pragma unroll
-    for (int c = 0; c < 8; ++c) {
-      const half8 v = __builtin_bit_cast(half8, src[c]);
-#pragma unroll
-      for (int e = 0; e < 8; ++e) xh[c * 8 + e] = v[e];
-    }
+    half8 hv = {};
+    if (i < p) hv = __builtin_bit_cast(half8, *reinterpret_cast<const uint4*>(d.qkv + (row0 + i) * ld + (size_t)which * E + h * HD + d0));
     if (which == 2) {
 #pragma unroll
-      for (int dd = 0; dd < HD; ++dd) Vt[dd * LDV + i] = xh[dd];
+      for (int e = 0; e < 8; ++e) Vt[(d0 + e) * LDV + i] = hv[e];
       continue;
     }
-    float x[HD];
+    float x[8];
     float ss = 0.0f;
 #pragma unroll
-    for (int dd = 0; dd < HD; ++dd) {
-      x[dd] = (float)xh[dd];
-      ss += x[dd] * x[dd];
+    for (int e = 0; e < 8; ++e) {
+      x[e] = (float)hv[e];
+      ss += x[e] * x[e];
     }
-    const float denom = sqrtf(ss / (float)HD + 1e-8f);
-    const float* nrm = which ? d.k_norm : d.q_norm;
+    ss += __shfl_xor(ss, 1);
+    ss += __shfl_xor(ss, 2);
+    ss += __shfl_xor(ss, 4);
+    half8 o = {};
+    if (i < p) {
+      const float inv = 1.0f / sqrtf(ss / (float)HD + 1e-8f);
+      const float* nrm = (which ? d.k_norm : d.q_norm) + d0;
+      const float* ct = d.rope_cos + (size_t)i * HD + d0;
+      const float* st = d.rope_sin + (size_t)i * HD + d0;
+      const float* xt = (which ? d.rope_scale_inv : d.rope_scale) + (size_t)i * HD + d0;
 #pragma unroll
-    for (int dd = 0; dd < HD; ++dd) x[dd] = (x[dd] / denom) * nrm[dd];
-    const float* ct = d.rope_cos + (size_t)i * HD;
-    const float* st = d.rope_sin + (size_t)i * HD;
-    const float* xt = d.rope_scale + (size_t)i * HD;
-    uint4* dst = reinterpret_cast<uint4*>((which ? Ks : Qs) + i * LDH);
-#pragma unroll
-    for (int c = 0; c < 8; ++c) {
-      half8 o;
+      for (int e = 0; e < 8; ++e) x[e] = (x[e] * inv) * nrm[e];
 #pragma unroll
       for (int e = 0; e < 8; ++e) {
-        const int dd = c * 8 + e;
-        const float sv = which ? 1.0f / xt[dd] : xt[dd];
-        const float rot = (dd & 1) ? x[dd - 1] : -x[dd + 1];
-        o[e] = (_Float16)(((x[dd] * ct[dd]) * sv) + ((rot * st[dd]) * sv));
+        const float rot = (e & 1) ? x[e - 1] : -x[e + 1];
+        o[e] = (_Float16)(((x[e] * ct[e]) * xt[e]) + ((rot * st[e]) * xt[e]));
       }
-      dst[c] = __builtin_bit_cast(uint4, o);
     }
+    *reinterpret_cast<uint4*>((which ? Ks : Qs) + i * LDH + d0) = __builtin_bit_cast(uint4, o);
   }
   __syncthreads();
 
@@ -295,16 +292,23 @@ void check_common(const AttnDesc& d) {
 void launch_time_attention(const AttnDesc& d, hipStream_t s) {
   if (d.v <= 0 || d.p <= 0) return;
   check_common(d);
-  if (!d.att || !d.fut || !d.rope_cos || !d.rope_sin || !d.rope_scale)
+  if (!d.att || !d.fut || !d.rope_cos || !d.rope_sin || !d.rope_scale || !d.rope_scale_inv)
     throw Error(T0H_ERR_INVALID_ARG, "time attention: null pointer");
   if (d.p > T0H_MAX_PATCHES)
     throw Error(T0H_ERR_UNSUPPORTED, "time attention: window of " + std::to_string(d.p) + " patches exceeds " +
                                          std::to_string(T0H_MAX_PATCHES));
   const size_t lds = time_attn_lds(d.p);
-  check_hip(hipFuncSetAttribute(reinterpret_cast<const void*>(&k_time_attn), hipFuncAttributeMaxDynamicSharedMemorySize,
-                                (int)lds),
-            "hipFuncSetAttribute(k_time_attn)");
-  hipLaunchKernelGGL(k_time_attn, dim3(d.v * d.heads), dim3(256), lds, s, d);
+  if (round_up(d.p, 32) / 16 <= 8) {
+    check_hip(hipFuncSetAttribute(reinterpret_cast<const void*>(&k_time_attn<8>),
+                                  hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds),
+              "hipFuncSetAttribute(k_time_attn)");
+    hipLaunchKernelGGL(k_time_attn<8>, dim3(d.v * d.heads), dim3(256), lds, s, d);
+  } else {
+    check_hip(hipFuncSetAttribute(reinterpret_cast<const void*>(&k_time_attn<MAXKT>),
+                                  hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds),
+              "hipFuncSetAttribute(k_time_attn)");
+    hipLaunchKernelGGL(k_time_attn<MAXKT>, dim3(d.v * d.heads), dim3(256), lds, s, d);
+  }
   check_hip(hipGetLastError(), "k_time_attn launch");
 }
 

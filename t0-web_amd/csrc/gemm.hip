@@ -4,8 +4,8 @@
 // Two kernels implement the t0-fast `linear()` contract (crates/t0-fast/src/
 // model.rs:406-504; ops.rs:40-42, y = x W^T + b):
 //
-//  * k_gemm — MFMA tile kernel for large M.  128x128 output tile per 256-thread
-//    workgroup (4 waves, 64x64 each, v_mfma_f32_16x16x32_f16).  Per 64-wide K
+//  * k_gemm — MFMA tile kernel for large M.  256x128 (M > 128) or 128x128 output
+//    tile per workgroup of 8 or 4 waves, 64x64 each, v_mfma_f32_16x16x32_f16.  Per 64-wide K
 //    step each thread fetches one 32-value weight block (34 B Q8_0 / 18 B Q4_0 /
 //    64 B f16) and one 32-value activation strip into registers while the
 //    previous step's MFMAs run, then dequantizes the block to f16 with packed
@@ -42,8 +42,7 @@ typedef _Float16 half4 __attribute__((ext_vector_type(4)));
 typedef _Float16 half2v __attribute__((ext_vector_type(2)));
 typedef float floatx4 __attribute__((ext_vector_type(4)));
 
-constexpr int TM = 128, TN = 128, TK = 64, LDK = TK + 8;
-constexpr int GEMM_LDS_BYTES = 2 * (TM + TN) * LDK * 2;
+constexpr int TN = 128, TK = 64, LDK = TK + 8;
 
 __host__ __device__ constexpr int block_bytes(int wt) { return wt == T0H_Q8_0 ? 34 : (wt == T0H_Q4_0 ? 18 : 0); }
 
@@ -70,16 +69,137 @@ __device__ __forceinline__ void q4x4_f16(uint32_t nib, half2v dd, uint32_t& o0, 
   o1 = __builtin_bit_cast(uint32_t, h1 * dd);
 }
 
-__device__ __forceinline__ float silu(float g) { return g / (1.0f + __expf(-g)); }
+// silu_mul.wgsl:21 g/(1+exp(-g)); reciprocal via v_rcp_f32 (output is rounded to f16).
+__device__ __forceinline__ float silu(float g) { return g * __builtin_amdgcn_rcpf(1.0f + __expf(-g)); }
 
 // ---------------------------------------------------------------------------
-// MFMA tile kernel
+// MFMA tile kernel.  NWM waves along M x 2 along N, each wave 64x64; tile
+// (64*NWM) x 128 x 64.  Loader roles: A strip = 32 activations per thread (row
+// tid/2, half tid%2); weights = 64/NWM values per thread.
 // ---------------------------------------------------------------------------
-template <int WT, bool A32, int EPI, bool AL4>
-__global__ __launch_bounds__(256) void k_gemm(const GemmDesc d) {
+template <int NWM>
+struct TileCfg {
+  static constexpr int BM = 64 * NWM, NT = 128 * NWM, BV = 64 / NWM;
+  static constexpr int LDS = 2 * (BM + TN) * LDK * 2;
+};
+
+// Loads the raw weight bytes of one thread's share of a K step.
+// BV == 32: one whole 32-value block (row tid/2, block tid%2).
+// BV == 16: Q8_0 / f16: half a block (16 consecutive values); Q4_0: 8 quant
+// bytes = values {8h..8h+7} and {16+8h..16+8h+7} of the block.
+template <int WT, bool AL4, int BV>
+__device__ __forceinline__ void load_w(const uint8_t* wrow, int kt, int part, uint32_t (&br)[16]) {
+  if (WT == T0H_F16) {
+    const uint4* src = reinterpret_cast<const uint4*>(wrow + (size_t)(kt * TK + part * BV) * 2);
+#pragma unroll
+    for (int i = 0; i < BV / 8; ++i) {
+      const uint4 v = src[i];
+      br[4 * i + 0] = v.x;
+      br[4 * i + 1] = v.y;
+      br[4 * i + 2] = v.z;
+      br[4 * i + 3] = v.w;
+    }
+    return;
+  }
+  constexpr int BB = block_bytes(WT);
+  if (BV == 32) {
+    const int lh = part;
+    if (AL4) {
+      const uint32_t* src = reinterpret_cast<const uint32_t*>(wrow) + (WT == T0H_Q8_0 ? 17 * kt + 8 * lh : 9 * kt + 4 * lh);
+      constexpr int NW = WT == T0H_Q8_0 ? 9 : 5;
+#pragma unroll
+      for (int i = 0; i < NW; ++i) br[i] = src[i];
+    } else {
+      const uint16_t* src = reinterpret_cast<const uint16_t*>(wrow + (size_t)(2 * kt + lh) * BB);
+      constexpr int NQ = WT == T0H_Q8_0 ? 8 : 4;
+      br[0] = src[0];
+#pragma unroll
+      for (int i = 0; i < NQ; ++i) br[1 + i] = (uint32_t)src[1 + 2 * i] | ((uint32_t)src[2 + 2 * i] << 16);
+    }
+    return;
+  }
+  // BV == 16: br[0] = scale dword, br[1..] = quant dwords (funnel-shifted in decode)
+  const int b = part >> 1, h = part & 1;
+  if (AL4) {
+    const uint32_t* base = reinterpret_cast<const uint32_t*>(wrow) + (WT == T0H_Q8_0 ? 17 * kt : 9 * kt);
+    if (WT == T0H_Q8_0) {
+      br[0] = base[b ? 8 : 0];
+      const uint32_t* q = base + (b ? 8 + 4 * h : 4 * h);
+#pragma unroll
+      for (int i = 0; i < 5; ++i) br[1 + i] = q[i];
+    } else {
+      br[0] = base[b ? 4 : 0];
+      const uint32_t* q = base + (b ? 4 + 2 * h : 2 * h);
+#pragma unroll
+      for (int i = 0; i < 3; ++i) br[1 + i] = q[i];
+    }
+  } else {
+    const uint16_t* src = reinterpret_cast<const uint16_t*>(wrow + (size_t)(2 * kt + b) * BB);
+    br[0] = src[0];
+    constexpr int NQ = WT == T0H_Q8_0 ? 4 : 2;  // dwords of quants
+    const uint16_t* q = src + 1 + (WT == T0H_Q8_0 ? 8 * h : 4 * h);
+#pragma unroll
+    for (int i = 0; i < NQ; ++i) br[1 + i] = (uint32_t)q[2 * i] | ((uint32_t)q[2 * i + 1] << 16);
+  }
+}
+
+// Dequantizes a thread's share to packed f16 (out[] in k order; for Q4_0 with
+// BV == 16, out[0..3] are the low-nibble values and out[4..7] the high ones).
+template <int WT, bool AL4, int BV>
+__device__ __forceinline__ void dequant_w(const uint32_t (&br)[16], int part, uint32_t (&out)[16]) {
+  if (WT == T0H_F16) {
+#pragma unroll
+    for (int i = 0; i < BV / 2; ++i) out[i] = br[i];
+    return;
+  }
+  uint32_t dbits, q[8];
+  constexpr int NQ = BV == 32 ? (WT == T0H_Q8_0 ? 8 : 4) : (WT == T0H_Q8_0 ? 4 : 2);
+  if (BV == 32) {
+    const int lh = part;
+    if (AL4) {
+      const uint32_t sel = lh ? 0x07060504u : 0x05040302u;
+      dbits = lh ? (br[0] >> 16) : (br[0] & 0xffffu);
+#pragma unroll
+      for (int i = 0; i < NQ; ++i) q[i] = perm(br[i + 1], br[i], sel);
+    } else {
+      dbits = br[0] & 0xffffu;
+#pragma unroll
+      for (int i = 0; i < NQ; ++i) q[i] = br[1 + i];
+    }
+  } else {
+    const int b = part >> 1;
+    if (AL4) {
+      dbits = b ? (br[0] >> 16) : (br[0] & 0xffffu);
+      const uint32_t sel = b ? 0x07060504u : 0x05040302u;
+#pragma unroll
+      for (int i = 0; i < NQ; ++i) q[i] = perm(br[i + 2], br[i + 1], sel);
+    } else {
+      dbits = br[0] & 0xffffu;
+#pragma unroll
+      for (int i = 0; i < NQ; ++i) q[i] = br[1 + i];
+    }
+  }
+  const _Float16 dh = __builtin_bit_cast(_Float16, (uint16_t)dbits);
+  const half2v dd = {dh, dh};
+  if (WT == T0H_Q8_0) {
+#pragma unroll
+    for (int i = 0; i < NQ; ++i) q8x4_f16(q[i], dd, out[2 * i], out[2 * i + 1]);
+  } else {
+#pragma unroll
+    for (int i = 0; i < NQ; ++i) {
+      q4x4_f16(q[i] & 0x0f0f0f0fu, dd, out[2 * i], out[2 * i + 1]);
+      q4x4_f16((q[i] >> 4) & 0x0f0f0f0fu, dd, out[2 * NQ + 2 * i], out[2 * NQ + 2 * i + 1]);
+    }
+  }
+}
+
+template <int WT, bool A32, int EPI, bool AL4, int NWM>
+__global__ __launch_bounds__(128 * NWM) void k_gemm(const GemmDesc d) {
+  using C = TileCfg<NWM>;
+  constexpr int BM = C::BM, BV = C::BV;
   extern __shared__ __align__(16) _Float16 smem[];
-  _Float16* As = smem;                 // [2][TM][LDK]
-  _Float16* Bs = smem + 2 * TM * LDK;  // [2][TN][LDK]
+  _Float16* As = smem;                 // [2][BM][LDK]
+  _Float16* Bs = smem + 2 * BM * LDK;  // [2][TN][LDK]
 
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int wm = wave >> 1, wn = wave & 1;
@@ -92,101 +212,71 @@ __global__ __launch_bounds__(256) void k_gemm(const GemmDesc d) {
   const int per = total / 8;
   const int logical = bid < per * 8 ? (bid % 8) * per + bid / 8 : bid;
   const int tm = logical / tiles_n, tn = logical % tiles_n;
-  const int m0 = tm * TM;
+  const int m0 = tm * BM;
 
-  // loader role: tile row lr, k half lh (32 values)
-  const int lr = tid >> 1, lh = tid & 1;
-  const int am = m0 + lr;
+  // A loader: row ar, half ah (32 values)
+  const int ar = tid >> 1, ah = tid & 1;
+  const int am = m0 + ar;
+  const bool avalid = am < M;
+  // weight loader: tile row br_, part bp
+  constexpr int PARTS = 64 / BV;
+  const int brow = tid / PARTS, bp = tid % PARTS;
   int wrow;
   bool bvalid;
   if (EPI == EPI_SWIGLU_F16) {
-    const int g = tn * 64 + (lr & 63);
+    const int g = tn * 64 + (brow & 63);
     bvalid = g < N;
-    wrow = lr < 64 ? g : N + g;  // gate rows then up rows (weight has 2N rows)
+    wrow = brow < 64 ? g : N + g;  // gate rows then up rows (weight has 2N rows)
   } else {
-    wrow = tn * TN + lr;
+    wrow = tn * TN + brow;
     bvalid = wrow < N;
   }
-  const bool avalid = am < M;
   const size_t rowb = WT == T0H_F16 ? (size_t)K * 2 : (size_t)(K / 32) * block_bytes(WT);
   const uint8_t* wbase = static_cast<const uint8_t*>(d.w) + (size_t)(bvalid ? wrow : 0) * rowb;
+  // k offset (in values) of this thread's weight share inside a K step
+  const int bk0 = BV == 32 ? bp * 32 : (WT == T0H_Q4_0 ? (bp >> 1) * 32 + (bp & 1) * 8 : bp * 16);
 
   uint32_t areg[A32 ? 32 : 16];
   uint32_t braw[16];
 
   auto load_global = [&](int kt) {
-    const int k0 = kt * TK + lh * 32;
-    const bool kin = k0 < K;
-    if (A32) {
-      if (avalid && kin) {
+    const int k0 = kt * TK + ah * 32;
+    if (avalid && k0 < K) {
+      if (A32) {
         const float4* src = reinterpret_cast<const float4*>(static_cast<const float*>(d.a) + (size_t)am * d.lda + k0);
 #pragma unroll
         for (int i = 0; i < 8; ++i) {
-          float4 v = src[i];
+          const float4 v = src[i];
           areg[4 * i + 0] = __builtin_bit_cast(uint32_t, v.x);
           areg[4 * i + 1] = __builtin_bit_cast(uint32_t, v.y);
           areg[4 * i + 2] = __builtin_bit_cast(uint32_t, v.z);
           areg[4 * i + 3] = __builtin_bit_cast(uint32_t, v.w);
         }
       } else {
-#pragma unroll
-        for (int i = 0; i < 32; ++i) areg[i] = 0;
-      }
-    } else {
-      if (avalid && kin) {
         const uint4* src = reinterpret_cast<const uint4*>(static_cast<const _Float16*>(d.a) + (size_t)am * d.lda + k0);
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
-          uint4 v = src[i];
+          const uint4 v = src[i];
           areg[4 * i + 0] = v.x;
           areg[4 * i + 1] = v.y;
           areg[4 * i + 2] = v.z;
           areg[4 * i + 3] = v.w;
         }
-      } else {
-#pragma unroll
-        for (int i = 0; i < 16; ++i) areg[i] = 0;
       }
+    } else {
+#pragma unroll
+      for (int i = 0; i < (A32 ? 32 : 16); ++i) areg[i] = 0;
     }
-    if (!(bvalid && kin)) {
+    if (bvalid && kt * TK + bk0 < K) {
+      load_w<WT, AL4, BV>(wbase, kt, bp, braw);
+    } else {
 #pragma unroll
       for (int i = 0; i < 16; ++i) braw[i] = 0;
-      return;
-    }
-    if (WT == T0H_F16) {
-      const uint4* src = reinterpret_cast<const uint4*>(wbase + (size_t)k0 * 2);
-#pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        uint4 v = src[i];
-        braw[4 * i + 0] = v.x;
-        braw[4 * i + 1] = v.y;
-        braw[4 * i + 2] = v.z;
-        braw[4 * i + 3] = v.w;
-      }
-    } else if (AL4) {
-      // rows are 4-byte aligned (K % 64 == 0): one block = dwords at a 2-byte phase
-      const uint32_t* src;
-      if (WT == T0H_Q8_0)
-        src = reinterpret_cast<const uint32_t*>(wbase) + 17 * kt + 8 * lh;
-      else
-        src = reinterpret_cast<const uint32_t*>(wbase) + 9 * kt + 4 * lh;
-      constexpr int NW = WT == T0H_Q8_0 ? 9 : 5;
-#pragma unroll
-      for (int i = 0; i < NW; ++i) braw[i] = src[i];
-    } else {
-      // general 2-byte aligned rows: scale + quants as u16
-      const uint16_t* src =
-          reinterpret_cast<const uint16_t*>(wbase + (size_t)(2 * kt + lh) * block_bytes(WT));
-      constexpr int NQ = WT == T0H_Q8_0 ? 8 : 4;
-      braw[0] = src[0];
-#pragma unroll
-      for (int i = 0; i < NQ; ++i) braw[1 + i] = (uint32_t)src[1 + 2 * i] | ((uint32_t)src[2 + 2 * i] << 16);
     }
   };
 
   auto store_lds = [&](int buf) {
     uint32_t out[16];
-    // A -> f16
     if (A32) {
 #pragma unroll
       for (int i = 0; i < 16; ++i) {
@@ -197,43 +287,20 @@ __global__ __launch_bounds__(256) void k_gemm(const GemmDesc d) {
 #pragma unroll
       for (int i = 0; i < 16; ++i) out[i] = areg[i];
     }
-    uint4* adst = reinterpret_cast<uint4*>(As + (size_t)buf * TM * LDK + lr * LDK + lh * 32);
+    uint4* adst = reinterpret_cast<uint4*>(As + (size_t)buf * BM * LDK + ar * LDK + ah * 32);
 #pragma unroll
     for (int i = 0; i < 4; ++i) adst[i] = make_uint4(out[4 * i], out[4 * i + 1], out[4 * i + 2], out[4 * i + 3]);
-    // B -> dequantized f16
-    if (WT == T0H_F16) {
-#pragma unroll
-      for (int i = 0; i < 16; ++i) out[i] = braw[i];
+    uint32_t wq[16];
+    dequant_w<WT, AL4, BV>(braw, bp, wq);
+    _Float16* brow_p = Bs + (size_t)buf * TN * LDK + brow * LDK;
+    if (BV == 16 && WT == T0H_Q4_0) {
+      *reinterpret_cast<uint4*>(brow_p + bk0) = make_uint4(wq[0], wq[1], wq[2], wq[3]);
+      *reinterpret_cast<uint4*>(brow_p + bk0 + 16) = make_uint4(wq[4], wq[5], wq[6], wq[7]);
     } else {
-      uint32_t dbits, q[8];
-      if (AL4) {
-        const uint32_t sel = lh ? 0x07060504u : 0x05040302u;
-        dbits = lh ? (braw[0] >> 16) : (braw[0] & 0xffffu);
-        constexpr int NQ = WT == T0H_Q8_0 ? 8 : 4;
 #pragma unroll
-        for (int i = 0; i < NQ; ++i) q[i] = perm(braw[i + 1], braw[i], sel);
-      } else {
-        dbits = braw[0] & 0xffffu;
-        constexpr int NQ = WT == T0H_Q8_0 ? 8 : 4;
-#pragma unroll
-        for (int i = 0; i < NQ; ++i) q[i] = braw[1 + i];
-      }
-      const _Float16 dh = __builtin_bit_cast(_Float16, (uint16_t)dbits);
-      const half2v dd = {dh, dh};
-      if (WT == T0H_Q8_0) {
-#pragma unroll
-        for (int i = 0; i < 8; ++i) q8x4_f16(q[i], dd, out[2 * i], out[2 * i + 1]);
-      } else {
-#pragma unroll
-        for (int i = 0; i < 4; ++i) {
-          q4x4_f16(q[i] & 0x0f0f0f0fu, dd, out[2 * i], out[2 * i + 1]);
-          q4x4_f16((q[i] >> 4) & 0x0f0f0f0fu, dd, out[8 + 2 * i], out[8 + 2 * i + 1]);
-        }
-      }
+      for (int i = 0; i < BV / 8; ++i)
+        reinterpret_cast<uint4*>(brow_p + bk0)[i] = make_uint4(wq[4 * i], wq[4 * i + 1], wq[4 * i + 2], wq[4 * i + 3]);
     }
-    uint4* bdst = reinterpret_cast<uint4*>(Bs + (size_t)buf * TN * LDK + lr * LDK + lh * 32);
-#pragma unroll
-    for (int i = 0; i < 4; ++i) bdst[i] = make_uint4(out[4 * i], out[4 * i + 1], out[4 * i + 2], out[4 * i + 3]);
   };
 
   // wave's B-tile rows for its 4 column sub-tiles
@@ -255,7 +322,7 @@ __global__ __launch_bounds__(256) void k_gemm(const GemmDesc d) {
   for (int kt = 0; kt < KT; ++kt) {
     const int buf = kt & 1;
     if (kt + 1 < KT) load_global(kt + 1);
-    const _Float16* At = As + (size_t)buf * TM * LDK;
+    const _Float16* At = As + (size_t)buf * BM * LDK;
     const _Float16* Bt = Bs + (size_t)buf * TN * LDK;
 #pragma unroll
     for (int ks = 0; ks < 2; ++ks) {
@@ -523,19 +590,31 @@ void check_hip(hipError_t e, const char* what) {
   if (e != hipSuccess) throw Error(T0H_ERR_HIP, std::string(what) + ": " + hipGetErrorString(e));
 }
 
-template <int WT, bool A32, int EPI, bool AL4>
+template <int WT, bool A32, int EPI, bool AL4, int NWM>
 void run_gemm(const GemmDesc& d, hipStream_t s) {
+  using C = TileCfg<NWM>;
   const int tiles_n = EPI == EPI_SWIGLU_F16 ? (d.N + 63) / 64 : (d.N + TN - 1) / TN;
-  const int tiles_m = (d.M + TM - 1) / TM;
+  const int tiles_m = (d.M + C::BM - 1) / C::BM;
   static bool attr_set = false;  // per instantiation
   if (!attr_set) {
-    check_hip(hipFuncSetAttribute(reinterpret_cast<const void*>(&k_gemm<WT, A32, EPI, AL4>),
-                                  hipFuncAttributeMaxDynamicSharedMemorySize, GEMM_LDS_BYTES),
+    check_hip(hipFuncSetAttribute(reinterpret_cast<const void*>(&k_gemm<WT, A32, EPI, AL4, NWM>),
+                                  hipFuncAttributeMaxDynamicSharedMemorySize, C::LDS),
               "hipFuncSetAttribute(k_gemm)");
     attr_set = true;
   }
-  hipLaunchKernelGGL((k_gemm<WT, A32, EPI, AL4>), dim3(tiles_m * tiles_n), dim3(256), GEMM_LDS_BYTES, s, d);
+  hipLaunchKernelGGL((k_gemm<WT, A32, EPI, AL4, NWM>), dim3(tiles_m * tiles_n), dim3(C::NT), C::LDS, s, d);
   check_hip(hipGetLastError(), "k_gemm launch");
+}
+
+// 256-row tiles halve the dequant work per MFMA but hold one workgroup per CU,
+// so the workgroups run in lock-step; measured faster only for the f16-store
+// (QKV) shape at config-4 scale.
+template <int WT, bool A32, int EPI, bool AL4>
+void run_gemm_m(const GemmDesc& d, hipStream_t s) {
+  if (EPI == EPI_STORE_F16 && d.M > 4096)
+    run_gemm<WT, A32, EPI, AL4, 4>(d, s);
+  else
+    run_gemm<WT, A32, EPI, AL4, 2>(d, s);
 }
 
 template <int WT, bool A32, int EPI, int MT>
@@ -565,9 +644,9 @@ void dispatch_w(const GemmDesc& d, int force, hipStream_t s) {
   const bool mfma = force == 1 || (force == 0 && d.M > 16);
   if (mfma) {
     if (WT != T0H_F16 && d.K % 64 == 0)
-      run_gemm<WT, A32, EPI, true>(d, s);
+      run_gemm_m<WT, A32, EPI, true>(d, s);
     else
-      run_gemm<WT, A32, EPI, false>(d, s);
+      run_gemm_m<WT, A32, EPI, false>(d, s);
   } else {
     dispatch_gemv<WT, A32, EPI>(d, s);
   }

@@ -53,7 +53,8 @@ struct AttnDesc {
   const float* k_norm = nullptr;
   const float* rope_cos = nullptr;  // [p, head_dim]
   const float* rope_sin = nullptr;
-  const float* rope_scale = nullptr;
+  const float* rope_scale = nullptr;      // xpos scale applied to q
+  const float* rope_scale_inv = nullptr;  // its reciprocal, applied to k (ops.rs:135-139)
   const int* grp = nullptr;          // [v*p] patch group id (-1 = all-PAD patch)
   const uint8_t* att = nullptr;      // [v*p] patch attendable
   const uint8_t* fut = nullptr;      // [v] row is FUTURE (bidirectional time attention)
@@ -88,11 +89,9 @@ struct PatchOut {
   float* patch_loc = nullptr;  // [v*p] scaler loc at each patch's last step (may be null)
   float* patch_scale = nullptr;
 };
-// Causal Welford scaler per row (scaler.rs:91-118), loc/scale per step into loc/scale [v*t].
-void launch_window_welford(const WindowDesc& w, float* loc, float* scale, hipStream_t s);
-// Patch encoder input + patch metadata from the window and its loc/scale.
-void launch_window_patchify(const WindowDesc& w, const float* loc, const float* scale, const PatchOut& o,
-                            hipStream_t s);
+// Window construction + causal scaler (scaler.rs:44-118) + patch encoder input and
+// metadata, one workgroup per row.
+void launch_window_prep(const WindowDesc& w, const PatchOut& o, hipStream_t s);
 // Same from an explicit (already padded and scaled) series on device.
 struct SeriesDev {
   const float* variates = nullptr;

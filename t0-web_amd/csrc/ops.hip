@@ -73,34 +73,6 @@ __device__ __forceinline__ Step window_step(const WindowDesc& w, int r, int s) {
   return st;
 }
 
-// scaler.rs:91-118 causal_row_stats, one thread per row.  Every operation is an
-// explicitly rounded IEEE op so no multiply-add is fused (Rust never contracts).
-__global__ __launch_bounds__(64) void k_welford(const WindowDesc w, float* loc, float* scale) {
-  const int r = blockIdx.x * 64 + threadIdx.x;
-  if (r >= w.v) return;
-  float count = 0.0f, mean = 0.0f, m2 = 0.0f;
-  const size_t base = (size_t)r * w.t;
-  for (int s = 0; s < w.t; ++s) {
-    const Step st = window_step(w, r, s);
-    if (st.mask == T0H_MASK_VALID) {
-      count = __fadd_rn(count, 1.0f);
-      const float delta = __fsub_rn(st.x, mean);
-      mean = __fadd_rn(mean, __fdiv_rn(delta, count));
-      const float delta2 = __fsub_rn(st.x, mean);
-      m2 = __fadd_rn(m2, __fmul_rn(delta, delta2));
-    }
-    const float var = count > 1.0f ? fmaxf(__fdiv_rn(m2, __fsub_rn(count, 1.0f)), 0.0f) : 0.0f;
-    float sc = w.variance_offset ? __fsqrt_rn(__fadd_rn(var, w.eps)) : fmaxf(__fsqrt_rn(var), w.eps);
-    float lc = mean;
-    if (st.group < 0) {  // padding sentinel (scaler.rs:56-62)
-      lc = 0.0f;
-      sc = 1.0f;
-    }
-    loc[base + s] = lc;
-    scale[base + s] = sc;
-  }
-}
-
 // Rust 1.99 std f32::asinh: ln_1p(ax + ax / (hypot(1, 1/ax) + 1/ax)) with x's sign.
 __device__ __forceinline__ float rust_asinh(float x) {
   const float ax = fabsf(x);
@@ -130,34 +102,119 @@ __device__ __forceinline__ void write_patch_meta(const PatchOut& o, size_t m, co
   o.att[m] = a.any ? 1 : 0;                 // mask.rs:32-43
 }
 
-// One thread per (row, patch): scaled values (scaler.rs:80-84) + [vals | k/ps | valid]
-// encoder input (model.rs:185-197) + patch metadata + loc/scale at the patch end.
-__global__ __launch_bounds__(256) void k_window_patchify(const WindowDesc w, const float* loc, const float* scale,
-                                                         const PatchOut o) {
-  const int p = w.t / w.ps;
-  const long long m = (long long)blockIdx.x * 256 + threadIdx.x;
-  if (m >= (long long)w.v * p) return;
-  const int r = (int)(m / p), pi = (int)(m % p), ps = w.ps;
-  _Float16* enc = o.enc_in + m * 3 * ps;
-  PatchAcc acc;
-  for (int k = 0; k < ps; ++k) {
-    const int s = pi * ps + k;
-    const Step st = window_step(w, r, s);
-    acc.add(st.mask, st.group, st.type);
-    const size_t ti = (size_t)r * w.t + s;
-    const float z = __fdiv_rn(__fsub_rn(st.x, loc[ti]), scale[ti]);
-    const float val = w.use_arcsinh ? rust_asinh(z) : z;
-    enc[k] = (_Float16)val;
-    enc[ps + k] = (_Float16)((float)k / (float)ps);
-    enc[2 * ps + k] = (_Float16)(st.mask == T0H_MASK_VALID ? 1.0f : 0.0f);
+// Welford state (count, mean, M2) and the pairwise merge of two disjoint
+// segments (Chan, Golub & LeVeque), used to give each thread the exact running
+// state at the start of its chunk.
+struct Wf {
+  float n, mean, m2;
+};
+__device__ __forceinline__ Wf wf_merge(Wf a, Wf b) {
+  const float n = a.n + b.n;
+  if (n == 0.0f) return a;
+  const float delta = b.mean - a.mean;
+  const float fb = b.n / n;
+  return {n, a.mean + delta * fb, a.m2 + b.m2 + delta * delta * (a.n * fb)};
+}
+
+// One 256-thread workgroup per row: window construction (padding, NaN ->
+// MISSING, ragged lead), the causal scaler (scaler.rs:44-118: Welford over VALID
+// steps, emitted after each step's update, variance m2/(n-1), eps per mode, pad
+// sentinel loc 0 / scale 1, then asinh), the patch encoder input [vals | k/ps |
+// valid] (model.rs:185-197) and the patch metadata (mask.rs:12-43), with each
+// patch's loc/scale at its last step for the rescale (scaler.rs:125-148).
+// Each thread runs the reference's sequential Welford recurrence over its own
+// chunk of steps, starting from the merged state of all earlier chunks.
+__global__ __launch_bounds__(256) void k_prep_rows(const WindowDesc w, const PatchOut o) {
+  extern __shared__ __align__(16) float psm[];
+  const int t = w.t, ps = w.ps, p = t / ps, r = blockIdx.x, tid = threadIdx.x;
+  float* xs = psm;             // [t] VALID value, NaN otherwise
+  float* scv = xs + t;         // [t] scaled value
+  float* pl = scv + t;         // [p] loc at patch end
+  float* psc = pl + p;         // [p] scale at patch end
+  Wf* st = reinterpret_cast<Wf*>(psc + p);  // [2][256] scan buffers
+
+  for (int s = tid; s < t; s += 256) {
+    const Step stp = window_step(w, r, s);
+    xs[s] = stp.mask == T0H_MASK_VALID ? stp.x : NAN;
   }
-  write_patch_meta(o, m, acc);
-  if (o.patch_loc) {
-    const size_t te = (size_t)r * w.t + pi * ps + ps - 1;
-    o.patch_loc[m] = loc[te];
-    o.patch_scale[m] = scale[te];
+  __syncthreads();
+  const int C = (t + 255) / 256;
+  const int s0 = min(t, tid * C), s1 = min(t, s0 + C);
+  Wf loc_state{0.0f, 0.0f, 0.0f};
+  for (int s = s0; s < s1; ++s) {
+    const float x = xs[s];
+    if (!isnan(x)) {
+      loc_state.n += 1.0f;
+      const float delta = x - loc_state.mean;
+      loc_state.mean += delta / loc_state.n;
+      loc_state.m2 += delta * (x - loc_state.mean);
+    }
+  }
+  // inclusive scan of chunk states (Hillis-Steele, ping-pong)
+  st[tid] = loc_state;
+  __syncthreads();
+  int cur = 0;
+  for (int off = 1; off < 256; off <<= 1) {
+    Wf v = st[cur * 256 + tid];
+    if (tid >= off) v = wf_merge(st[cur * 256 + tid - off], v);
+    st[(cur ^ 1) * 256 + tid] = v;
+    cur ^= 1;
+    __syncthreads();
+  }
+  Wf state = tid > 0 ? st[cur * 256 + tid - 1] : Wf{0.0f, 0.0f, 0.0f};
+  for (int s = s0; s < s1; ++s) {
+    const float x = xs[s];
+    const bool valid = !isnan(x);
+    if (valid) {
+      state.n += 1.0f;
+      const float delta = x - state.mean;
+      state.mean += delta / state.n;
+      state.m2 += delta * (x - state.mean);
+    }
+    const float var = state.n > 1.0f ? fmaxf(state.m2 / (state.n - 1.0f), 0.0f) : 0.0f;
+    float sc = w.variance_offset ? sqrtf(var + w.eps) : fmaxf(sqrtf(var), w.eps);
+    float lc = state.mean;
+    if (window_step(w, r, s).group < 0) {  // padding sentinel (scaler.rs:56-62)
+      lc = 0.0f;
+      sc = 1.0f;
+    }
+    const float z = __fdiv_rn(__fsub_rn(valid ? x : 0.0f, lc), sc);
+    scv[s] = w.use_arcsinh ? rust_asinh(z) : z;
+    if (s % ps == ps - 1) {
+      pl[s / ps] = lc;
+      psc[s / ps] = sc;
+    }
+  }
+  __syncthreads();
+  const size_t m0 = (size_t)r * p;
+  _Float16* enc = o.enc_in + m0 * 3 * ps;
+  for (int idx = tid; idx < p * 3 * ps; idx += 256) {
+    const int pi = idx / (3 * ps), f = idx % (3 * ps);
+    float val;
+    if (f < ps)
+      val = scv[pi * ps + f];
+    else if (f < 2 * ps)
+      val = (float)(f - ps) / (float)ps;
+    else
+      val = isnan(xs[pi * ps + f - 2 * ps]) ? 0.0f : 1.0f;
+    enc[idx] = (_Float16)val;
+  }
+  for (int pi = tid; pi < p; pi += 256) {
+    PatchAcc acc;
+    for (int k = 0; k < ps; ++k) {
+      const Step stp = window_step(w, r, pi * ps + k);
+      acc.add(stp.mask, stp.group, stp.type);
+    }
+    write_patch_meta(o, m0 + pi, acc);
+    if (o.patch_loc) {
+      o.patch_loc[m0 + pi] = pl[pi];
+      o.patch_scale[m0 + pi] = psc[pi];
+    }
+    if (pi == 0) o.fut[r] = acc.type == T0H_VT_FUTURE ? 1 : 0;  // mask.rs:52
   }
 }
+
+size_t prep_lds(int t, int ps) { return (size_t)(2 * t + 2 * (t / ps)) * 4 + 2 * 256 * sizeof(Wf); }
 
 __global__ __launch_bounds__(256) void k_series_patchify(const SeriesDev sd, const PatchOut o) {
   const int p = sd.t / sd.ps;
@@ -265,21 +322,19 @@ void launch_rmsnorm(const float* x, const float* scale, _Float16* out, const int
   check_hip(hipGetLastError(), "k_rmsnorm launch");
 }
 
-void launch_window_welford(const WindowDesc& w, float* loc, float* scale, hipStream_t s) {
+void launch_window_prep(const WindowDesc& w, const PatchOut& o, hipStream_t s) {
   if (w.v <= 0) return;
-  if (!w.ctx || !w.src_off || !w.len || !w.group || !loc || !scale) throw Error(T0H_ERR_INVALID_ARG, "welford: null");
-  hipLaunchKernelGGL(k_welford, dim3(blocks(w.v, 64)), dim3(64), 0, s, w, loc, scale);
-  check_hip(hipGetLastError(), "k_welford launch");
-}
-
-void launch_window_patchify(const WindowDesc& w, const float* loc, const float* scale, const PatchOut& o,
-                            hipStream_t s) {
-  if (w.v <= 0) return;
-  if (w.ps <= 0 || w.t % w.ps) throw Error(T0H_ERR_SHAPE, "patchify: window not patch aligned");
-  if (!o.enc_in || !o.grp || !o.att || !o.type_idx || !o.type_raw) throw Error(T0H_ERR_INVALID_ARG, "patchify: null");
-  const long long n = (long long)w.v * (w.t / w.ps);
-  hipLaunchKernelGGL(k_window_patchify, dim3(blocks(n, 256)), dim3(256), 0, s, w, loc, scale, o);
-  check_hip(hipGetLastError(), "k_window_patchify launch");
+  if (!w.ctx || !w.src_off || !w.len || !w.group) throw Error(T0H_ERR_INVALID_ARG, "prep: null window arrays");
+  if (w.ps <= 0 || w.t % w.ps) throw Error(T0H_ERR_SHAPE, "prep: window not patch aligned");
+  if (!o.enc_in || !o.grp || !o.att || !o.type_idx || !o.type_raw || !o.fut)
+    throw Error(T0H_ERR_INVALID_ARG, "prep: null output arrays");
+  const size_t lds = prep_lds(w.t, w.ps);
+  if (lds > 160 * 1024) throw Error(T0H_ERR_UNSUPPORTED, "prep: window too long for one workgroup");
+  check_hip(hipFuncSetAttribute(reinterpret_cast<const void*>(&k_prep_rows), hipFuncAttributeMaxDynamicSharedMemorySize,
+                                (int)lds),
+            "hipFuncSetAttribute(k_prep_rows)");
+  hipLaunchKernelGGL(k_prep_rows, dim3(w.v), dim3(256), lds, s, w, o);
+  check_hip(hipGetLastError(), "k_prep_rows launch");
 }
 
 void launch_series_patchify(const SeriesDev& sd, const PatchOut& o, hipStream_t s) {

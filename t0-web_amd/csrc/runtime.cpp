@@ -417,6 +417,9 @@ void ensure_rope(t0h_model* m, int p) {
   put(m, "rope_cos", a.data(), a.size());
   put(m, "rope_sin", b.data(), b.size());
   put(m, "rope_scale", c.data(), c.size());
+  std::vector<float> ci(c.size());
+  for (size_t i = 0; i < c.size(); ++i) ci[i] = 1.0f / c[i];  // k-side table, scale.recip() in f32
+  put(m, "rope_scale_inv", ci.data(), ci.size());
   m->ws.rope_p = p;
 }
 
@@ -499,6 +502,7 @@ void encode_and_layers(t0h_model* m, int v, int p, const PatchMeta& pm, float* t
   ad.rope_cos = ws_get<float>(m, "rope_cos", (size_t)p * 64);
   ad.rope_sin = ws_get<float>(m, "rope_sin", (size_t)p * 64);
   ad.rope_scale = ws_get<float>(m, "rope_scale", (size_t)p * 64);
+  ad.rope_scale_inv = ws_get<float>(m, "rope_scale_inv", (size_t)p * 64);
   ad.grp = pm.grp;
   ad.att = pm.att;
   ad.fut = pm.fut;
@@ -615,18 +619,11 @@ void forecast_window(t0h_model* m, const WindowRows& wr, float* d_out) {
   w.use_arcsinh = c.scaler_use_arcsinh;
   w.variance_offset = c.scaler_variance_offset;
   w.eps = c.scaler_eps;
-  float* loc = ws_get<float>(m, "loc", (size_t)v * t);
-  float* scl = ws_get<float>(m, "scale", (size_t)v * t);
   PatchMeta pm = patch_buffers(m, v, p);
   {
-    ProfScope ps_(m, "prep_welford");
-    launch_window_welford(w, loc, scl, s);
-  }
-  {
-    ProfScope ps_(m, "prep_patchify");
+    ProfScope ps_(m, "prep");
     PatchOut po{pm.enc_in, pm.grp, pm.att, pm.type_idx, pm.type_raw, pm.fut, pm.patch_loc, pm.patch_scale};
-    launch_window_patchify(w, loc, scl, po, s);
-    launch_fut_rows(pm.type_raw, pm.fut, v, p, s);
+    launch_window_prep(w, po, s);
   }
   encode_and_layers(m, v, p, pm, nullptr, nullptr);
   if (hp == 0) return;
