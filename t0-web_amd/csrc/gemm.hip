@@ -41,6 +41,7 @@ typedef _Float16 half8 __attribute__((ext_vector_type(8)));
 typedef _Float16 half4 __attribute__((ext_vector_type(4)));
 typedef _Float16 half2v __attribute__((ext_vector_type(2)));
 typedef float floatx4 __attribute__((ext_vector_type(4)));
+typedef float floatx16 __attribute__((ext_vector_type(16)));
 
 constexpr int TN = 128, TK = 64, LDK = TK + 8;
 
@@ -194,7 +195,7 @@ __device__ __forceinline__ void dequant_w(const uint32_t (&br)[16], int part, ui
 }
 
 template <int WT, bool A32, int EPI, bool AL4, int NWM>
-__global__ __launch_bounds__(128 * NWM) void k_gemm(const GemmDesc d) {
+__global__ __launch_bounds__(128 * NWM) __attribute__((amdgpu_waves_per_eu(2, 2))) void k_gemm(const GemmDesc d) {
   using C = TileCfg<NWM>;
   constexpr int BM = C::BM, BV = C::BV;
   extern __shared__ __align__(16) _Float16 smem[];
@@ -214,13 +215,13 @@ __global__ __launch_bounds__(128 * NWM) void k_gemm(const GemmDesc d) {
   const int tm = logical / tiles_n, tn = logical % tiles_n;
   const int m0 = tm * BM;
 
-  // A loader: row ar, half ah (32 values)
+  // A loader: row ar, half ah (32 values); rows past M read row M-1
   const int ar = tid >> 1, ah = tid & 1;
-  const int am = m0 + ar;
-  const bool avalid = am < M;
-  // weight loader: tile row br_, part bp
+  const int amc = min(m0 + ar, M - 1);
+  // weight loader: tile row brow, part bp; rows past N read row 0
   constexpr int PARTS = 64 / BV;
   const int brow = tid / PARTS, bp = tid % PARTS;
+  const int bp_lo = bp & (PARTS / 2 - 1);  // the same share of the step's first block
   int wrow;
   bool bvalid;
   if (EPI == EPI_SWIGLU_F16) {
@@ -236,62 +237,73 @@ __global__ __launch_bounds__(128 * NWM) void k_gemm(const GemmDesc d) {
   // k offset (in values) of this thread's weight share inside a K step
   const int bk0 = BV == 32 ? bp * 32 : (WT == T0H_Q4_0 ? (bp >> 1) * 32 + (bp & 1) * 8 : bp * 16);
 
-  uint32_t areg[A32 ? 32 : 16];
-  uint32_t braw[16];
-
-  auto load_global = [&](int kt) {
-    const int k0 = kt * TK + ah * 32;
-    if (avalid && k0 < K) {
-      if (A32) {
-        const float4* src = reinterpret_cast<const float4*>(static_cast<const float*>(d.a) + (size_t)am * d.lda + k0);
-#pragma unroll
-        for (int i = 0; i < 8; ++i) {
-          const float4 v = src[i];
-          areg[4 * i + 0] = __builtin_bit_cast(uint32_t, v.x);
-          areg[4 * i + 1] = __builtin_bit_cast(uint32_t, v.y);
-          areg[4 * i + 2] = __builtin_bit_cast(uint32_t, v.z);
-          areg[4 * i + 3] = __builtin_bit_cast(uint32_t, v.w);
-        }
-      } else {
-        const uint4* src = reinterpret_cast<const uint4*>(static_cast<const _Float16*>(d.a) + (size_t)am * d.lda + k0);
-#pragma unroll
-        for (int i = 0; i < 4; ++i) {
-          const uint4 v = src[i];
-          areg[4 * i + 0] = v.x;
-          areg[4 * i + 1] = v.y;
-          areg[4 * i + 2] = v.z;
-          areg[4 * i + 3] = v.w;
-        }
-      }
-    } else {
-#pragma unroll
-      for (int i = 0; i < (A32 ? 32 : 16); ++i) areg[i] = 0;
-    }
-    if (bvalid && kt * TK + bk0 < K) {
-      load_w<WT, AL4, BV>(wbase, kt, bp, braw);
-    } else {
-#pragma unroll
-      for (int i = 0; i < 16; ++i) braw[i] = 0;
-    }
+  // Raw global data of one K step held in registers between its load and its
+  // LDS store.  Two stages are in flight: the loads for step kt+2 are issued
+  // while step kt is multiplied, so a fresh activation strip (which every
+  // workgroup of an XCD requests at the same time) has two steps of MFMA work
+  // to arrive from HBM.
+  struct Stage {
+    uint32_t a[A32 ? 32 : 16];
+    uint32_t b[16];
   };
 
-  auto store_lds = [&](int buf) {
+  // Branch-free loads: rows past M or N read a clamped valid row (their
+  // outputs are never stored); only the K tail of the last step (K % 64 == 32)
+  // is zeroed, under a uniform branch, so the stage stays in registers.
+  auto load_global = [&](Stage& st, int kt) {
+    const int k0 = kt * TK + ah * 32;
+    const int k0c = k0 < K ? k0 : k0 - 32;
+    if (A32) {
+      const float4* src = reinterpret_cast<const float4*>(static_cast<const float*>(d.a) + (size_t)amc * d.lda + k0c);
+#pragma unroll
+      for (int i = 0; i < 8; ++i) {
+        const float4 v = src[i];
+        st.a[4 * i + 0] = __builtin_bit_cast(uint32_t, v.x);
+        st.a[4 * i + 1] = __builtin_bit_cast(uint32_t, v.y);
+        st.a[4 * i + 2] = __builtin_bit_cast(uint32_t, v.z);
+        st.a[4 * i + 3] = __builtin_bit_cast(uint32_t, v.w);
+      }
+    } else {
+      const uint4* src = reinterpret_cast<const uint4*>(static_cast<const _Float16*>(d.a) + (size_t)amc * d.lda + k0c);
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const uint4 v = src[i];
+        st.a[4 * i + 0] = v.x;
+        st.a[4 * i + 1] = v.y;
+        st.a[4 * i + 2] = v.z;
+        st.a[4 * i + 3] = v.w;
+      }
+    }
+    load_w<WT, AL4, BV>(wbase, kt, kt * TK + bk0 < K ? bp : bp_lo, st.b);
+  };
+
+  auto store_lds = [&](Stage& st, int buf, int kt) {
+    if (kt * TK + TK > K) {  // uniform: the last step of a K % 64 == 32 problem
+      const bool aok = kt * TK + ah * 32 < K;
+#pragma unroll
+      for (int i = 0; i < (A32 ? 32 : 16); ++i) st.a[i] = aok ? st.a[i] : 0u;
+    }
     uint32_t out[16];
     if (A32) {
 #pragma unroll
       for (int i = 0; i < 16; ++i) {
-        half2v h = {(_Float16)__builtin_bit_cast(float, areg[2 * i]), (_Float16)__builtin_bit_cast(float, areg[2 * i + 1])};
+        half2v h = {(_Float16)__builtin_bit_cast(float, st.a[2 * i]), (_Float16)__builtin_bit_cast(float, st.a[2 * i + 1])};
         out[i] = __builtin_bit_cast(uint32_t, h);
       }
     } else {
 #pragma unroll
-      for (int i = 0; i < 16; ++i) out[i] = areg[i];
+      for (int i = 0; i < 16; ++i) out[i] = st.a[i];
     }
     uint4* adst = reinterpret_cast<uint4*>(As + (size_t)buf * BM * LDK + ar * LDK + ah * 32);
 #pragma unroll
     for (int i = 0; i < 4; ++i) adst[i] = make_uint4(out[4 * i], out[4 * i + 1], out[4 * i + 2], out[4 * i + 3]);
+    const bool bok = kt * TK + bk0 < K;
     uint32_t wq[16];
-    dequant_w<WT, AL4, BV>(braw, bp, wq);
+    dequant_w<WT, AL4, BV>(st.b, bok ? bp : bp_lo, wq);
+    if (kt * TK + TK > K) {
+#pragma unroll
+      for (int i = 0; i < BV / 2; ++i) wq[i] = bok ? wq[i] : 0u;
+    }
     _Float16* brow_p = Bs + (size_t)buf * TN * LDK + brow * LDK;
     if (BV == 16 && WT == T0H_Q4_0) {
       *reinterpret_cast<uint4*>(brow_p + bk0) = make_uint4(wq[0], wq[1], wq[2], wq[3]);
@@ -303,92 +315,140 @@ __global__ __launch_bounds__(128 * NWM) void k_gemm(const GemmDesc d) {
     }
   };
 
-  // wave's B-tile rows for its 4 column sub-tiles
-  int bcol[4];
+  // Each wave owns a 64x64 block as 2x2 tiles of v_mfma_f32_32x32x16_f16
+  // (measured on MI355X: this shape sustains ~2.2 PFLOP/s even at one wave per
+  // SIMD, where 16x16x32 needs 16+ independent chains and several waves).
+  // Operand lane layout: lane l holds row (A) / column (B) l%32 and k-slots
+  // (l/32)*8 .. +8 of the 16-wide K slice.
+  // B-tile rows of the wave's two column tiles; SwiGLU pairs gate tile j=0 with
+  // the up tile j=1 holding the same hidden columns.
+  int bcol[2];
 #pragma unroll
-  for (int j = 0; j < 4; ++j)
-    bcol[j] = EPI == EPI_SWIGLU_F16 ? ((j < 2) ? wn * 32 + j * 16 : 64 + wn * 32 + (j - 2) * 16) : wn * 64 + j * 16;
+  for (int j = 0; j < 2; ++j)
+    bcol[j] = EPI == EPI_SWIGLU_F16 ? j * 64 + wn * 32 : wn * 64 + j * 32;
 
-  floatx4 acc[4][4];
+  floatx16 acc[2][2];
 #pragma unroll
-  for (int i = 0; i < 4; ++i)
+  for (int i = 0; i < 2; ++i)
 #pragma unroll
-    for (int j = 0; j < 4; ++j) acc[i][j] = (floatx4){0.f, 0.f, 0.f, 0.f};
+    for (int j = 0; j < 2; ++j)
+#pragma unroll
+      for (int e = 0; e < 16; ++e) acc[i][j][e] = 0.0f;
 
-  const int KT = (K + TK - 1) / TK;
-  load_global(0);
-  store_lds(0);
-  __syncthreads();
-  for (int kt = 0; kt < KT; ++kt) {
-    const int buf = kt & 1;
-    if (kt + 1 < KT) load_global(kt + 1);
-    const _Float16* At = As + (size_t)buf * BM * LDK;
-    const _Float16* Bt = Bs + (size_t)buf * TN * LDK;
+  auto compute = [&](int buf) {
+    const _Float16* At = As + (size_t)buf * BM * LDK + (wm * 64 + (lane & 31)) * LDK + (lane >> 5) * 8;
+    const _Float16* Bt = Bs + (size_t)buf * TN * LDK + (lane & 31) * LDK + (lane >> 5) * 8;
 #pragma unroll
-    for (int ks = 0; ks < 2; ++ks) {
-      half8 af[4], bf[4];
-      const int koff = ks * 32 + (lane >> 4) * 8;
+    for (int kk = 0; kk < TK / 16; ++kk) {
+      half8 af[2], bf[2];
 #pragma unroll
-      for (int i = 0; i < 4; ++i)
-        af[i] = *reinterpret_cast<const half8*>(At + (wm * 64 + i * 16 + (lane & 15)) * LDK + koff);
+      for (int i = 0; i < 2; ++i) af[i] = *reinterpret_cast<const half8*>(At + i * 32 * LDK + kk * 16);
 #pragma unroll
-      for (int j = 0; j < 4; ++j) bf[j] = *reinterpret_cast<const half8*>(Bt + (bcol[j] + (lane & 15)) * LDK + koff);
+      for (int j = 0; j < 2; ++j) bf[j] = *reinterpret_cast<const half8*>(Bt + bcol[j] * LDK + kk * 16);
 #pragma unroll
-      for (int i = 0; i < 4; ++i)
+      for (int i = 0; i < 2; ++i)
 #pragma unroll
-        for (int j = 0; j < 4; ++j) acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(af[i], bf[j], acc[i][j], 0, 0, 0);
+        for (int j = 0; j < 2; ++j) acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(af[i], bf[j], acc[i][j], 0, 0, 0);
     }
-    if (kt + 1 < KT) store_lds(buf ^ 1);
+  };
+
+  // Steps alternate between (LDS buffer 0, stage s0) and (buffer 1, stage s1);
+  // the loop body covers two steps so the stage registers are indexed statically.
+  const int KT = (K + TK - 1) / TK;
+  Stage s0, s1;
+  load_global(s0, 0);
+  if (KT > 1) load_global(s1, 1);
+  store_lds(s0, 0, 0);
+  __syncthreads();
+  for (int kt = 0; kt < KT; kt += 2) {
+    if (kt + 2 < KT) load_global(s0, kt + 2);
+    compute(0);
+    if (kt + 1 < KT) store_lds(s1, 1, kt + 1);
+    __syncthreads();
+    if (kt + 1 >= KT) break;
+    if (kt + 3 < KT) load_global(s1, kt + 3);
+    compute(1);
+    if (kt + 2 < KT) store_lds(s0, 0, kt + 2);
     __syncthreads();
   }
 
-  // epilogue: lane holds rows (lane>>4)*4 + e, column lane&15 of each 16x16 sub-tile
-  const int rbase = m0 + wm * 64 + (lane >> 4) * 4;
-  if (EPI == EPI_SWIGLU_F16) {
-    _Float16* y = static_cast<_Float16*>(d.y);
+  // Epilogue, staged through LDS (free after the main loop's last barrier):
+  // each wave writes a 32-row slice of its results (bias, SwiGLU applied) as
+  // f32 into its own LDS region, then streams the slice out in 16-byte row
+  // chunks (coalesced f32/f16 stores, vector residual read-modify-write).
+  // In each 32x32 MFMA tile lane l holds column l%32, rows (e/4)*8 + (l/32)*4 + e%4.
+  constexpr int W = EPI == EPI_SWIGLU_F16 ? 32 : 64;  // output columns per wave
+  constexpr int SLD = W + 4;                          // staging row stride (floats)
+  float* stage = reinterpret_cast<float*>(smem) + wave * 32 * SLD;
+  const int cbase = EPI == EPI_SWIGLU_F16 ? tn * 64 + wn * 32 : tn * TN + wn * 64;  // first output column
+  const int lc = lane & 31, lr = (lane >> 5) * 4;
+  float bj[2];
 #pragma unroll
-    for (int j = 0; j < 2; ++j) {
-      const int g = tn * 64 + wn * 32 + j * 16 + (lane & 15);
-      if (g >= N) continue;
-      const float bg = d.bias ? d.bias[g] : 0.0f, bu = d.bias ? d.bias[N + g] : 0.0f;
+  for (int j = 0; j < 2; ++j) {
+    const int col = EPI == EPI_SWIGLU_F16 ? cbase + lc + (j ? N : 0) : cbase + j * 32 + lc;
+    bj[j] = (d.bias && (EPI == EPI_SWIGLU_F16 ? cbase + lc < N : col < N)) ? d.bias[col] : 0.0f;
+  }
+  const bool vec_ok = (d.ldy & 3) == 0 && (N & 3) == 0;
 #pragma unroll
-      for (int i = 0; i < 4; ++i)
+  for (int i = 0; i < 2; ++i) {
 #pragma unroll
-        for (int e = 0; e < 4; ++e) {
-          const int row = rbase + i * 16 + e;
-          if (row < M) {
-            const float gate = acc[i][j][e] + bg, up = acc[i][j + 2][e] + bu;
-            y[(size_t)row * d.ldy + g] = (_Float16)(silu(gate) * up);
-          }
-        }
+    for (int e = 0; e < 16; ++e) {
+      const int r = (e >> 2) * 8 + lr + (e & 3);
+      if (EPI == EPI_SWIGLU_F16) {
+        stage[r * SLD + lc] = silu(acc[i][0][e] + bj[0]) * (acc[i][1][e] + bj[1]);
+      } else {
+        stage[r * SLD + lc] = acc[i][0][e] + bj[0];
+        stage[r * SLD + 32 + lc] = acc[i][1][e] + bj[1];
+      }
     }
-  } else {
+    __syncthreads();
+    const int row0 = m0 + wm * 64 + i * 32;
 #pragma unroll
-    for (int j = 0; j < 4; ++j) {
-      const int col = tn * TN + bcol[j] + (lane & 15);
-      if (col >= N) continue;
-      const float b = d.bias ? d.bias[col] : 0.0f;
+    for (int t = 0; t < 32 * W / 4 / 64; ++t) {
+      const int idx = t * 64 + lane;
+      const int r = idx / (W / 4), c = (idx % (W / 4)) * 4;
+      const int row = row0 + r, col = cbase + c;
+      if (row >= M || col >= N) continue;
+      float4 v = *reinterpret_cast<const float4*>(stage + r * SLD + c);
+      const size_t o = (size_t)row * d.ldy + col;
+      if (vec_ok) {
+        if (EPI == EPI_STORE_F32 && d.row_add) {
+          const float4 t4 = *reinterpret_cast<const float4*>(d.row_add + (size_t)d.row_add_idx[row] * N + col);
+          v.x += t4.x; v.y += t4.y; v.z += t4.z; v.w += t4.w;
+        }
+        if (EPI != EPI_RESID_F32 && d.relu) {
+          v.x = fmaxf(v.x, 0.0f); v.y = fmaxf(v.y, 0.0f); v.z = fmaxf(v.z, 0.0f); v.w = fmaxf(v.w, 0.0f);
+        }
+        if (EPI == EPI_RESID_F32) {
+          float4* y = reinterpret_cast<float4*>(static_cast<float*>(d.y) + o);
+          const float4 old = *y;
+          *y = make_float4(old.x + v.x, old.y + v.y, old.z + v.z, old.w + v.w);
+        } else if (EPI == EPI_STORE_F32) {
+          *reinterpret_cast<float4*>(static_cast<float*>(d.y) + o) = v;
+        } else {
+          half4 h = {(_Float16)v.x, (_Float16)v.y, (_Float16)v.z, (_Float16)v.w};
+          *reinterpret_cast<half4*>(static_cast<_Float16*>(d.y) + o) = h;
+        }
+      } else {
+        const float vv[4] = {v.x, v.y, v.z, v.w};
 #pragma unroll
-      for (int i = 0; i < 4; ++i)
-#pragma unroll
-        for (int e = 0; e < 4; ++e) {
-          const int row = rbase + i * 16 + e;
-          if (row >= M) continue;
-          float v = acc[i][j][e] + b;
-          const size_t o = (size_t)row * d.ldy + col;
+        for (int q = 0; q < 4; ++q) {
+          if (col + q >= N) break;
+          float x = vv[q];
+          if (EPI == EPI_STORE_F32 && d.row_add) x += d.row_add[(size_t)d.row_add_idx[row] * N + col + q];
+          if (EPI != EPI_RESID_F32 && d.relu) x = fmaxf(x, 0.0f);
           if (EPI == EPI_RESID_F32) {
-            float* y = static_cast<float*>(d.y);
-            y[o] = y[o] + v;
+            float* y = static_cast<float*>(d.y) + o + q;
+            *y = *y + x;
+          } else if (EPI == EPI_STORE_F32) {
+            static_cast<float*>(d.y)[o + q] = x;
           } else {
-            if (EPI == EPI_STORE_F32 && d.row_add) v = v + d.row_add[(size_t)d.row_add_idx[row] * N + col];
-            if (d.relu) v = v > 0.0f ? v : 0.0f;
-            if (EPI == EPI_STORE_F32)
-              static_cast<float*>(d.y)[o] = v;
-            else
-              static_cast<_Float16*>(d.y)[o] = (_Float16)v;
+            static_cast<_Float16*>(d.y)[o + q] = (_Float16)x;
           }
         }
+      }
     }
+    if (i == 0) __syncthreads();
   }
 }
 
