@@ -146,7 +146,85 @@ def cpu_baseline(gguf, x, groups, t_ctx, horizon, budget_s=12.0):
                       f"{dt:.1f} s"}
 
 
+# Device kernel behind each profiled GEMM kind of the forward (template args:
+# weight type 2 = Q4_0 / 8 = Q8_0, f32 activations, epilogue 1 f16 store / 3 SwiGLU).
+KERNEL_OF = {("gemm_w0_swiglu", "q4_0"): "k_gemm<2, false, 3,", ("gemm_w0_swiglu", "q8_0"): "k_gemm<8, false, 3,",
+             ("gemm_qkv", "q4_0"): "k_gemm<2, false, 1,", ("gemm_qkv", "q8_0"): "k_gemm<8, false, 1,"}
+COPY_BYTES = 256 << 20  # the --calibrate-copy kernel reads and writes this many bytes
+TRAFFIC_FILE = os.path.join(ROOT, "profiles", "traffic_config4.json")
+
+
+def _pmc_per_dispatch(d):
+    """{dispatch_id: (kernel_name, grid, value)} from a rocprofv3 --pmc csv directory."""
+    import csv
+    import glob
+    out = {}
+    for f in glob.glob(os.path.join(d, "**", "*counter_collection.csv"), recursive=True):
+        for r in csv.DictReader(open(f)):
+            k = (f, r["Dispatch_Id"])
+            name, grid, v = out.get(k, (r["Kernel_Name"], int(r["Grid_Size"]), 0.0))
+            out[k] = (name, grid, v + float(r["Counter_Value"]))
+    return out
+
+
+def traffic_of(kind, quant):
+    """HBM bytes per launch of `kind`'s kernel from the committed --pmc summary, or None."""
+    try:
+        rec = json.load(open(TRAFFIC_FILE))
+    except (OSError, ValueError):
+        return None
+    return rec.get("traffic") if (rec.get("kind"), rec.get("quant")) == (kind, quant) else None
+
+
+def summarize(prof_dir, fetch_dir, write_dir, quant, kind):
+    """Summaries of a --kernel-trace --stats run and two --pmc runs (FETCH_SIZE, WRITE_SIZE;
+    KiB per dispatch) of this script: per-kernel time table and the HBM traffic of `kind`'s
+    kernel, each counter scaled by what it reads for the 256 MiB calibration copy."""
+    import csv
+    import glob
+    lines = []
+    stats = glob.glob(os.path.join(prof_dir, "**", "*kernel_stats.csv"), recursive=True)
+    if stats:
+        rows = list(csv.DictReader(open(stats[0])))
+        rows.sort(key=lambda r: -float(r["TotalDurationNs"]))
+        lines += ["| kernel | calls | total us | avg us | % |", "|---|---|---|---|---|"]
+        for r in rows[:16]:
+            lines.append(f"| `{r['Name'][:110]}` | {r['Calls']} | {float(r['TotalDurationNs']) / 1e3:.1f} | "
+                         f"{float(r['AverageNs']) / 1e3:.2f} | {float(r['Percentage']):.2f} |")
+    res = {"kind": kind, "quant": quant}
+    for ctr, d in (("FETCH_SIZE", fetch_dir), ("WRITE_SIZE", write_dir)):
+        disp = _pmc_per_dispatch(d)
+        copies = [v for (n, g, v) in disp.values() if "copyBuffer" in n and v * 1024 > COPY_BYTES / 4]
+        if not copies:
+            raise SystemExit(f"{d}: no calibration copy dispatch (run with --calibrate-copy)")
+        factor = COPY_BYTES / (max(copies) * 1024)
+        vals = [v for (n, g, v) in disp.values() if KERNEL_OF[(kind, quant)] in n]
+        if not vals:
+            raise SystemExit(f"{d}: no dispatch of {KERNEL_OF[(kind, quant)]}")
+        per = sum(vals) / len(vals) * 1024 * factor
+        res[ctr.lower()] = {"kib_per_dispatch_raw": round(sum(vals) / len(vals), 1), "copy_factor": round(factor, 3),
+                            "bytes_per_launch": int(per), "dispatches": len(vals)}
+    res["traffic"] = res["fetch_size"]["bytes_per_launch"] + res["write_size"]["bytes_per_launch"]
+    lines += ["", f"HBM traffic of `{KERNEL_OF[(kind, quant)]} ...>` ({kind}, {quant}) per launch:",
+              f"FETCH_SIZE {res['fetch_size']['kib_per_dispatch_raw']} KiB x {res['fetch_size']['copy_factor']} "
+              f"+ WRITE_SIZE {res['write_size']['kib_per_dispatch_raw']} KiB x {res['write_size']['copy_factor']} "
+              f"= {res['traffic'] / 1e6:.1f} MB"]
+    return "\n".join(lines), res
+
+
 def main():
+    if len(sys.argv) > 1 and sys.argv[1] == "--summarize":
+        sp = argparse.ArgumentParser()
+        sp.add_argument("--summarize", nargs=3, metavar=("PROF_DIR", "FETCH_DIR", "WRITE_DIR"), required=True)
+        sp.add_argument("--quant", default="q4_0", choices=["q4_0", "q8_0"])
+        sp.add_argument("--kind", default="gemm_w0_swiglu")
+        sp.add_argument("--traffic-out", default=None, help="write the traffic record (JSON) here")
+        a = sp.parse_args()
+        text, res = summarize(*a.summarize, a.quant, a.kind)
+        print(text)
+        if a.traffic_out:
+            json.dump(res, open(a.traffic_out, "w"), indent=1)
+        return
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=20)
@@ -219,7 +297,7 @@ def main():
     flops = gemm_flops(dom, M, cfg)
     achieved = flops / avg_s * 1e-12
     roofline = {"kernel": dom, "bound": "mfma", "achieved": round(achieved, 1), "peak": MFMA_F16_PEAK_TFLOPS,
-                "unit": "TFLOP/s", "frac": round(achieved / MFMA_F16_PEAK_TFLOPS, 4), "traffic": None,
+                "unit": "TFLOP/s", "frac": round(achieved / MFMA_F16_PEAK_TFLOPS, 4), "traffic": traffic_of(dom, args.quant),
                 "flops_per_launch": flops, "algorithmic_bytes_per_launch": int(gemm_bytes(dom, M, cfg, bpv)),
                 "avg_launch_us": round(avg_s * 1e6, 2)}
     total_gemm_flops = sum(gemm_flops(k, M, cfg) * prof[k][0] for k in gemm_names) / args.profile_steps

@@ -12,6 +12,18 @@
  * restatement is pinned by the reference's own known-answer tests, an
  * independent numpy restatement of the quant codec, closed forms and
  * brute-force checks (see tests/).
+ *
+ * Parity unpinned (at the f32 rounding level only; every function below is
+ * pinned to tolerance by a closed form or the float64 numpy forward):
+ *   - t0r_linear's summation order.  The reference sums through
+ *     matrixmultiply 0.3.11 (burn-ndarray 0.20.1 -> ndarray 0.17.2), which is
+ *     absent here; this file uses a fixed 8-way split dot.
+ *   - the f32 forms of silu, softplus and softmax inside t0r_forward (Burn
+ *     0.20.1's are absent; the t0-fast WGSL forms silu_mul.wgsl:21,
+ *     quantile_head.wgsl:19 and attention.wgsl:53-65 are restated), and the
+ *     reduction order of the mean of squares in t0r_rmsnorm.
+ *   - t0r_rope_tables' f64 pow/cos/sin (C libm here, Rust std there; at most
+ *     one f64 ulp apart before the f32 cast).
  */
 #ifndef T0REF_H
 #define T0REF_H

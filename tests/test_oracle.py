@@ -278,3 +278,32 @@ def test_horizon_limit(tiny_oracle, oracle):
     with pytest.raises(oracle.OracleError) as e:
         tiny_oracle.forecast(np.zeros((1, 64), np.float32), 1, 64, 1025)
     assert e.value.code == -9
+
+
+def test_grouped_is_per_group_forecast(tiny_oracle):
+    """Grouped batch (one group id per row) equals t0_core::forecast on each group's rows alone:
+    groups never see each other (mask.rs:49-82) and share one window (lib.rs:50-97)."""
+    rng = np.random.default_rng(10)
+    ctx = sine_mix(rng, 5, 160)
+    ctx[3, 40:90] = np.nan
+    groups = np.array([7, 7, 2, 2, 2], np.int64)
+    g = tiny_oracle.forecast_grouped(ctx, groups, 160, 48)
+    for rows in ([0, 1], [2, 3, 4]):
+        s = tiny_oracle.forecast(ctx[rows], len(rows), 160, 48)
+        assert np.max(np.abs(g[rows] - s)) <= 1e-5
+
+
+def test_grouped_ar_is_repeated_forecast(tiny_oracle):
+    """Each AR step appends the median-level forecast (the level closest to 0.5) to every row and
+    forecasts again from the trailing t_ctx values, as forecast_rollout does (model.rs:582-665)."""
+    rng = np.random.default_rng(11)
+    t_ctx, h = 128, 32
+    ctx = sine_mix(rng, 4, t_ctx)
+    groups = np.array([0, 0, 1, 1], np.int64)
+    ar = tiny_oracle.forecast_grouped_ar(ctx, groups, t_ctx, h, 3)
+    qi = int(np.argmin(np.abs(np.asarray(tiny_oracle.levels) - 0.5)))
+    cur = ctx.copy()
+    for step in range(3):
+        f = tiny_oracle.forecast_grouped(cur, groups, t_ctx, h)
+        assert np.array_equal(ar[:, step * h:(step + 1) * h], f)
+        cur = np.concatenate([cur, f[:, :, qi]], axis=1)[:, -t_ctx:]
