@@ -4,13 +4,13 @@
 // Two kernels implement the t0-fast `linear()` contract (crates/t0-fast/src/
 // model.rs:406-504; ops.rs:40-42, y = x W^T + b):
 //
-//  * k_gemm — MFMA tile kernel for large M.  256x128 (M > 128) or 128x128 output
-//    tile per workgroup of 8 or 4 waves, 64x64 each, v_mfma_f32_16x16x32_f16.  Per 64-wide K
-//    step each thread fetches one 32-value weight block (34 B Q8_0 / 18 B Q4_0 /
-//    64 B f16) and one 32-value activation strip into registers while the
-//    previous step's MFMAs run, then dequantizes the block to f16 with packed
-//    f16 math (exact integer-to-f16 via the 0x6400 exponent trick, then one
-//    rounding of d*q) into a double-buffered LDS tile.  Accumulation is f32.
+//  * k_gemm — MFMA tile kernel for large M: 128x128, 256x128 or 256x256 output
+//    tiles per 4-wave workgroup, v_mfma_f32_32x32x16_f16.  Per 64-wide K step
+//    each thread fetches 32-value weight blocks (34 B Q8_0 / 18 B Q4_0 / 64 B
+//    f16) and 32-value activation strips into registers two steps ahead, then
+//    dequantizes the blocks to f16 with packed f16 math (exact integer-to-f16
+//    via the 0x6400 exponent trick, then one rounding of d*q) into a
+//    double-buffered LDS tile.  Accumulation is f32.
 //    Fused epilogues: bias, ReLU, f16/f32 store, residual add into the f32
 //    stream, SwiGLU (gate column j paired with up column H+j in one tile), and a
 //    row-gathered table add (type embeddings).  Workgroups are remapped so that
@@ -74,26 +74,32 @@ __device__ __forceinline__ void q4x4_f16(uint32_t nib, half2v dd, uint32_t& o0, 
 __device__ __forceinline__ float silu(float g) { return g * __builtin_amdgcn_rcpf(1.0f + __expf(-g)); }
 
 // ---------------------------------------------------------------------------
-// MFMA tile kernel.  NWM waves along M x 2 along N, each wave 64x64; tile
-// (64*NWM) x 128 x 64.  Loader roles: A strip = 32 activations per thread (row
-// tid/2, half tid%2); weights = 64/NWM values per thread.
+// MFMA tile kernel.  Four waves (2 x 2); each wave owns TI x TJ tiles of
+// v_mfma_f32_32x32x16_f16, so the workgroup tile is (64*TI) x (64*TJ) x 64.
+// Larger wave tiles cut LDS bytes per flop (the main loop's limiter): 128x128
+// waves (TI = TJ = 4) read half the LDS bytes per MFMA of 64x64 waves, and
+// keep their 256 accumulators in AGPRs at one wave per SIMD.
+// Measured on MI355X: 32x32x16 sustains ~2.2 PFLOP/s even at one wave per SIMD,
+// where 16x16x32 needs 16+ independent chains and several waves.
 // ---------------------------------------------------------------------------
-template <int NWM>
-struct TileCfg {
-  static constexpr int BM = 64 * NWM, NT = 128 * NWM, BV = 64 / NWM;
-  static constexpr int LDS = 2 * (BM + TN) * LDK * 2;
+template <int TI, int TJ>
+struct Tile {
+  static constexpr int BM = 64 * TI, BN = 64 * TJ;    // workgroup tile
+  static constexpr int RA = BM / 128, RB = BN / 128;  // A / weight rows per loader thread
+  static constexpr int WPE = TI * TJ > 4 ? 1 : 2;     // waves per SIMD the registers allow
+  static constexpr int LDS_MAIN = 2 * (BM + BN) * LDK * 2;
+  static constexpr int LDS_EPI = 4 * 32 * (TJ * 32 + 4) * 4;
+  static constexpr int LDS = LDS_MAIN > LDS_EPI ? LDS_MAIN : LDS_EPI;
 };
 
-// Loads the raw weight bytes of one thread's share of a K step.
-// BV == 32: one whole 32-value block (row tid/2, block tid%2).
-// BV == 16: Q8_0 / f16: half a block (16 consecutive values); Q4_0: 8 quant
-// bytes = values {8h..8h+7} and {16+8h..16+8h+7} of the block.
-template <int WT, bool AL4, int BV>
+// Raw bytes of one thread's weight share of a K step: half of the step (one
+// 32-value block, `part` 0 or 1) of one row.
+template <int WT, bool AL4>
 __device__ __forceinline__ void load_w(const uint8_t* wrow, int kt, int part, uint32_t (&br)[16]) {
   if (WT == T0H_F16) {
-    const uint4* src = reinterpret_cast<const uint4*>(wrow + (size_t)(kt * TK + part * BV) * 2);
+    const uint4* src = reinterpret_cast<const uint4*>(wrow + (size_t)(kt * TK + part * 32) * 2);
 #pragma unroll
-    for (int i = 0; i < BV / 8; ++i) {
+    for (int i = 0; i < 4; ++i) {
       const uint4 v = src[i];
       br[4 * i + 0] = v.x;
       br[4 * i + 1] = v.y;
@@ -103,82 +109,41 @@ __device__ __forceinline__ void load_w(const uint8_t* wrow, int kt, int part, ui
     return;
   }
   constexpr int BB = block_bytes(WT);
-  if (BV == 32) {
-    const int lh = part;
-    if (AL4) {
-      const uint32_t* src = reinterpret_cast<const uint32_t*>(wrow) + (WT == T0H_Q8_0 ? 17 * kt + 8 * lh : 9 * kt + 4 * lh);
-      constexpr int NW = WT == T0H_Q8_0 ? 9 : 5;
+  if (AL4) {  // the step's two blocks start 4-byte aligned: dword loads, realigned in dequant_w
+    const uint32_t* src = reinterpret_cast<const uint32_t*>(wrow) + (WT == T0H_Q8_0 ? 17 * kt + 8 * part : 9 * kt + 4 * part);
+    constexpr int NW = WT == T0H_Q8_0 ? 9 : 5;
 #pragma unroll
-      for (int i = 0; i < NW; ++i) br[i] = src[i];
-    } else {
-      const uint16_t* src = reinterpret_cast<const uint16_t*>(wrow + (size_t)(2 * kt + lh) * BB);
-      constexpr int NQ = WT == T0H_Q8_0 ? 8 : 4;
-      br[0] = src[0];
-#pragma unroll
-      for (int i = 0; i < NQ; ++i) br[1 + i] = (uint32_t)src[1 + 2 * i] | ((uint32_t)src[2 + 2 * i] << 16);
-    }
-    return;
-  }
-  // BV == 16: br[0] = scale dword, br[1..] = quant dwords (funnel-shifted in decode)
-  const int b = part >> 1, h = part & 1;
-  if (AL4) {
-    const uint32_t* base = reinterpret_cast<const uint32_t*>(wrow) + (WT == T0H_Q8_0 ? 17 * kt : 9 * kt);
-    if (WT == T0H_Q8_0) {
-      br[0] = base[b ? 8 : 0];
-      const uint32_t* q = base + (b ? 8 + 4 * h : 4 * h);
-#pragma unroll
-      for (int i = 0; i < 5; ++i) br[1 + i] = q[i];
-    } else {
-      br[0] = base[b ? 4 : 0];
-      const uint32_t* q = base + (b ? 4 + 2 * h : 2 * h);
-#pragma unroll
-      for (int i = 0; i < 3; ++i) br[1 + i] = q[i];
-    }
+    for (int i = 0; i < NW; ++i) br[i] = src[i];
   } else {
-    const uint16_t* src = reinterpret_cast<const uint16_t*>(wrow + (size_t)(2 * kt + b) * BB);
+    const uint16_t* src = reinterpret_cast<const uint16_t*>(wrow + (size_t)(2 * kt + part) * BB);
+    constexpr int NQ = WT == T0H_Q8_0 ? 8 : 4;
     br[0] = src[0];
-    constexpr int NQ = WT == T0H_Q8_0 ? 4 : 2;  // dwords of quants
-    const uint16_t* q = src + 1 + (WT == T0H_Q8_0 ? 8 * h : 4 * h);
 #pragma unroll
-    for (int i = 0; i < NQ; ++i) br[1 + i] = (uint32_t)q[2 * i] | ((uint32_t)q[2 * i + 1] << 16);
+    for (int i = 0; i < NQ; ++i) br[1 + i] = (uint32_t)src[1 + 2 * i] | ((uint32_t)src[2 + 2 * i] << 16);
   }
 }
 
-// Dequantizes a thread's share to packed f16 (out[] in k order; for Q4_0 with
-// BV == 16, out[0..3] are the low-nibble values and out[4..7] the high ones).
-template <int WT, bool AL4, int BV>
+// One block (32 values, k order) to packed f16 in out[0..15].
+template <int WT, bool AL4>
 __device__ __forceinline__ void dequant_w(const uint32_t (&br)[16], int part, uint32_t (&out)[16]) {
   if (WT == T0H_F16) {
 #pragma unroll
-    for (int i = 0; i < BV / 2; ++i) out[i] = br[i];
+    for (int i = 0; i < 16; ++i) out[i] = br[i];
     return;
   }
   uint32_t dbits, q[8];
-  constexpr int NQ = BV == 32 ? (WT == T0H_Q8_0 ? 8 : 4) : (WT == T0H_Q8_0 ? 4 : 2);
-  if (BV == 32) {
-    const int lh = part;
-    if (AL4) {
-      const uint32_t sel = lh ? 0x07060504u : 0x05040302u;
-      dbits = lh ? (br[0] >> 16) : (br[0] & 0xffffu);
+  constexpr int NQ = WT == T0H_Q8_0 ? 8 : 4;
+  if (AL4) {
+    // part 0: the block starts at byte 0 of br (scale in the low half of br[0]);
+    // part 1: at byte 2 (Q8_0 34 = 8*4+2, Q4_0 18 = 4*4+2), scale in the high half.
+    const uint32_t sel = part ? 0x07060504u : 0x05040302u;
+    dbits = part ? (br[0] >> 16) : (br[0] & 0xffffu);
 #pragma unroll
-      for (int i = 0; i < NQ; ++i) q[i] = perm(br[i + 1], br[i], sel);
-    } else {
-      dbits = br[0] & 0xffffu;
-#pragma unroll
-      for (int i = 0; i < NQ; ++i) q[i] = br[1 + i];
-    }
+    for (int i = 0; i < NQ; ++i) q[i] = perm(br[i + 1], br[i], sel);
   } else {
-    const int b = part >> 1;
-    if (AL4) {
-      dbits = b ? (br[0] >> 16) : (br[0] & 0xffffu);
-      const uint32_t sel = b ? 0x07060504u : 0x05040302u;
+    dbits = br[0] & 0xffffu;
 #pragma unroll
-      for (int i = 0; i < NQ; ++i) q[i] = perm(br[i + 2], br[i + 1], sel);
-    } else {
-      dbits = br[0] & 0xffffu;
-#pragma unroll
-      for (int i = 0; i < NQ; ++i) q[i] = br[1 + i];
-    }
+    for (int i = 0; i < NQ; ++i) q[i] = br[1 + i];
   }
   const _Float16 dh = __builtin_bit_cast(_Float16, (uint16_t)dbits);
   const half2v dd = {dh, dh};
@@ -188,188 +153,330 @@ __device__ __forceinline__ void dequant_w(const uint32_t (&br)[16], int part, ui
   } else {
 #pragma unroll
     for (int i = 0; i < NQ; ++i) {
-      q4x4_f16(q[i] & 0x0f0f0f0fu, dd, out[2 * i], out[2 * i + 1]);
-      q4x4_f16((q[i] >> 4) & 0x0f0f0f0fu, dd, out[2 * NQ + 2 * i], out[2 * NQ + 2 * i + 1]);
+      q4x4_f16(q[i] & 0x0f0f0f0fu, dd, out[2 * i], out[2 * i + 1]);                 // values 4i..4i+3
+      q4x4_f16((q[i] >> 4) & 0x0f0f0f0fu, dd, out[8 + 2 * i], out[8 + 2 * i + 1]);  // values 16+4i..
     }
   }
 }
 
-template <int WT, bool A32, int EPI, bool AL4, int NWM>
-__global__ __launch_bounds__(128 * NWM) __attribute__((amdgpu_waves_per_eu(2, 2))) void k_gemm(const GemmDesc d) {
-  using C = TileCfg<NWM>;
-  constexpr int BM = C::BM, BV = C::BV;
+// The same dequantization split into chunks (one quant dword each) so the
+// VALU work can be spread between MFMAs.  Q8_0: 8 chunks of 4 values;
+// Q4_0: 4 chunks of 8 values (4 low nibbles -> k 4c.., 4 high -> k 16+4c..).
+template <int WT>
+constexpr int dq_chunks() { return WT == T0H_Q8_0 ? 8 : (WT == T0H_Q4_0 ? 4 : 0); }
+
+template <int WT, bool AL4>
+__device__ __forceinline__ half2v dq_scale(const uint32_t (&br)[16], int part) {
+  const uint32_t dbits = AL4 ? (part ? (br[0] >> 16) : (br[0] & 0xffffu)) : (br[0] & 0xffffu);
+  const _Float16 dh = __builtin_bit_cast(_Float16, (uint16_t)dbits);
+  return half2v{dh, dh};
+}
+
+template <int WT, bool AL4>
+__device__ __forceinline__ void dq_chunk(const uint32_t (&br)[16], int part, int c, half2v dd, uint32_t (&out)[16]) {
+  const uint32_t q = AL4 ? perm(br[c + 1], br[c], part ? 0x07060504u : 0x05040302u) : br[1 + c];
+  if (WT == T0H_Q8_0) {
+    q8x4_f16(q, dd, out[2 * c], out[2 * c + 1]);
+    asm volatile("" : "+v"(out[2 * c]), "+v"(out[2 * c + 1]));  // keep the chunk here
+  } else {
+    q4x4_f16(q & 0x0f0f0f0fu, dd, out[2 * c], out[2 * c + 1]);
+    q4x4_f16((q >> 4) & 0x0f0f0f0fu, dd, out[8 + 2 * c], out[8 + 2 * c + 1]);
+    asm volatile("" : "+v"(out[2 * c]), "+v"(out[2 * c + 1]), "+v"(out[8 + 2 * c]), "+v"(out[8 + 2 * c + 1]));
+  }
+}
+
+template <int WT, bool A32, int EPI, bool K64, int TI, int TJ>
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(Tile<TI, TJ>::WPE, Tile<TI, TJ>::WPE)))
+void k_gemm(const GemmDesc d) {
+  using C = Tile<TI, TJ>;
+  constexpr int BM = C::BM, BN = C::BN, RA = C::RA, RB = C::RB;
+  constexpr bool SWI = EPI == EPI_SWIGLU_F16;
+  constexpr int HB = SWI ? BN / 2 : BN;  // output columns per tile (SwiGLU: gate rows then up rows)
   extern __shared__ __align__(16) _Float16 smem[];
   _Float16* As = smem;                 // [2][BM][LDK]
-  _Float16* Bs = smem + 2 * BM * LDK;  // [2][TN][LDK]
+  _Float16* Bs = smem + 2 * BM * LDK;  // [2][BN][LDK]
 
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int wm = wave >> 1, wn = wave & 1;
   const int M = d.M, N = d.N, K = d.K;
-  const int tiles_n = EPI == EPI_SWIGLU_F16 ? (N + 63) / 64 : (N + TN - 1) / TN;
+  const int tiles_n = (N + HB - 1) / HB;
 
   // XCD-aware remap: blocks are dispatched round-robin over 8 XCDs; give each
-  // XCD a contiguous range of logical tiles (N fastest within an M strip).
+  // XCD a contiguous range of logical tiles (N fastest within an M strip), so
+  // an activation strip is fetched once per XCD and shared through its L2.
   const int total = gridDim.x, bid = blockIdx.x;
   const int per = total / 8;
   const int logical = bid < per * 8 ? (bid % 8) * per + bid / 8 : bid;
   const int tm = logical / tiles_n, tn = logical % tiles_n;
   const int m0 = tm * BM;
 
-  // A loader: row ar, half ah (32 values); rows past M read row M-1
-  const int ar = tid >> 1, ah = tid & 1;
-  const int amc = min(m0 + ar, M - 1);
-  // weight loader: tile row brow, part bp; rows past N read row 0
-  constexpr int PARTS = 64 / BV;
-  const int brow = tid / PARTS, bp = tid % PARTS;
-  const int bp_lo = bp & (PARTS / 2 - 1);  // the same share of the step's first block
-  int wrow;
-  bool bvalid;
-  if (EPI == EPI_SWIGLU_F16) {
-    const int g = tn * 64 + (brow & 63);
-    bvalid = g < N;
-    wrow = brow < 64 ? g : N + g;  // gate rows then up rows (weight has 2N rows)
-  } else {
-    wrow = tn * TN + brow;
-    bvalid = wrow < N;
-  }
+  // Loader roles: thread t moves rows t/2 + 128 r of both tiles, half t%2 of
+  // each 64-wide K step (32 activations; one 32-value weight block).  Rows
+  // past M read row M-1 and weight rows past N read row 0: their outputs are
+  // never stored, and the loads stay branch-free.
+  const int lrow = tid >> 1, lh = tid & 1;
+  const char* abase[RA];
+#pragma unroll
+  for (int r = 0; r < RA; ++r)
+    abase[r] = static_cast<const char*>(d.a) + (size_t)min(m0 + lrow + 128 * r, M - 1) * d.lda * (A32 ? 4 : 2);
   const size_t rowb = WT == T0H_F16 ? (size_t)K * 2 : (size_t)(K / 32) * block_bytes(WT);
-  const uint8_t* wbase = static_cast<const uint8_t*>(d.w) + (size_t)(bvalid ? wrow : 0) * rowb;
-  // k offset (in values) of this thread's weight share inside a K step
-  const int bk0 = BV == 32 ? bp * 32 : (WT == T0H_Q4_0 ? (bp >> 1) * 32 + (bp & 1) * 8 : bp * 16);
+  const uint8_t* wbase[RB];
+#pragma unroll
+  for (int r = 0; r < RB; ++r) {
+    const int br = lrow + 128 * r;
+    int wrow;
+    bool ok;
+    if (SWI) {
+      const int g = tn * HB + (br % HB);
+      ok = g < N;
+      wrow = br < HB ? g : N + g;  // gate rows then up rows (the weight has 2N rows)
+    } else {
+      wrow = tn * BN + br;
+      ok = wrow < N;
+    }
+    wbase[r] = static_cast<const uint8_t*>(d.w) + (size_t)(ok ? wrow : 0) * rowb;
+  }
 
-  // Raw global data of one K step held in registers between its load and its
-  // LDS store.  Two stages are in flight: the loads for step kt+2 are issued
-  // while step kt is multiplied, so a fresh activation strip (which every
-  // workgroup of an XCD requests at the same time) has two steps of MFMA work
-  // to arrive from HBM.
+  // Raw global data of one K step, held in registers from its load to its LDS
+  // store.  Two steps are in flight (loads for kt+2 issue while kt multiplies).
   struct Stage {
-    uint32_t a[A32 ? 32 : 16];
-    uint32_t b[16];
+    uint32_t a[RA][A32 ? 32 : 16];
+    uint32_t b[RB][16];
   };
 
-  // Branch-free loads: rows past M or N read a clamped valid row (their
-  // outputs are never stored); only the K tail of the last step (K % 64 == 32)
-  // is zeroed, under a uniform branch, so the stage stays in registers.
+  // K64 (K % 64 == 0, the model's shapes): no K tail, so loads and stores are
+  // unconditional; otherwise the tail half of the last step reads the step's
+  // first half again and is zeroed at the store.
   auto load_global = [&](Stage& st, int kt) {
-    const int k0 = kt * TK + ah * 32;
-    const int k0c = k0 < K ? k0 : k0 - 32;
-    if (A32) {
-      const float4* src = reinterpret_cast<const float4*>(static_cast<const float*>(d.a) + (size_t)amc * d.lda + k0c);
+    const int k0 = kt * TK + lh * 32;
+    const int k0c = (K64 || k0 < K) ? k0 : k0 - 32;
 #pragma unroll
-      for (int i = 0; i < 8; ++i) {
-        const float4 v = src[i];
-        st.a[4 * i + 0] = __builtin_bit_cast(uint32_t, v.x);
-        st.a[4 * i + 1] = __builtin_bit_cast(uint32_t, v.y);
-        st.a[4 * i + 2] = __builtin_bit_cast(uint32_t, v.z);
-        st.a[4 * i + 3] = __builtin_bit_cast(uint32_t, v.w);
-      }
-    } else {
-      const uint4* src = reinterpret_cast<const uint4*>(static_cast<const _Float16*>(d.a) + (size_t)amc * d.lda + k0c);
+    for (int r = 0; r < RA; ++r) {
+      if (A32) {
+        const float4* src = reinterpret_cast<const float4*>(reinterpret_cast<const float*>(abase[r]) + k0c);
 #pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        const uint4 v = src[i];
-        st.a[4 * i + 0] = v.x;
-        st.a[4 * i + 1] = v.y;
-        st.a[4 * i + 2] = v.z;
-        st.a[4 * i + 3] = v.w;
+        for (int i = 0; i < 8; ++i) {
+          const float4 v = src[i];
+          st.a[r][4 * i + 0] = __builtin_bit_cast(uint32_t, v.x);
+          st.a[r][4 * i + 1] = __builtin_bit_cast(uint32_t, v.y);
+          st.a[r][4 * i + 2] = __builtin_bit_cast(uint32_t, v.z);
+          st.a[r][4 * i + 3] = __builtin_bit_cast(uint32_t, v.w);
+        }
+      } else {
+        const uint4* src = reinterpret_cast<const uint4*>(reinterpret_cast<const _Float16*>(abase[r]) + k0c);
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          const uint4 v = src[i];
+          st.a[r][4 * i + 0] = v.x;
+          st.a[r][4 * i + 1] = v.y;
+          st.a[r][4 * i + 2] = v.z;
+          st.a[r][4 * i + 3] = v.w;
+        }
       }
     }
-    load_w<WT, AL4, BV>(wbase, kt, kt * TK + bk0 < K ? bp : bp_lo, st.b);
+    const int part = (K64 || k0 < K) ? lh : 0;
+#pragma unroll
+    for (int r = 0; r < RB; ++r) load_w<WT, K64>(wbase[r], kt, part, st.b[r]);
   };
 
+  // A stage's registers -> f16 tile rows (A converted or copied, weights
+  // dequantized; the K tail zeroed), then into LDS buffer `buf`.
+  auto prep = [&](Stage& st, int kt, uint32_t (&ao)[RA][16], uint32_t (&wo)[RB][16]) {
+    const bool ok = K64 || kt * TK + lh * 32 < K;
+    const bool tail = !K64 && kt * TK + TK > K;  // uniform
+#pragma unroll
+    for (int r = 0; r < RA; ++r) {
+      if (A32) {
+#pragma unroll
+        for (int i = 0; i < 16; ++i) {
+          half2v h = {(_Float16)__builtin_bit_cast(float, st.a[r][2 * i]),
+                      (_Float16)__builtin_bit_cast(float, st.a[r][2 * i + 1])};
+          ao[r][i] = __builtin_bit_cast(uint32_t, h);
+        }
+      } else {
+#pragma unroll
+        for (int i = 0; i < 16; ++i) ao[r][i] = st.a[r][i];
+      }
+      if (tail) {
+#pragma unroll
+        for (int i = 0; i < 16; ++i) ao[r][i] = ok ? ao[r][i] : 0u;
+      }
+    }
+#pragma unroll
+    for (int r = 0; r < RB; ++r) {
+      dequant_w<WT, K64>(st.b[r], ok ? lh : 0, wo[r]);
+      if (tail) {
+#pragma unroll
+        for (int i = 0; i < 16; ++i) wo[r][i] = ok ? wo[r][i] : 0u;
+      }
+    }
+  };
+  auto write = [&](const uint32_t (&ao)[RA][16], const uint32_t (&wo)[RB][16], int buf) {
+#pragma unroll
+    for (int r = 0; r < RA; ++r) {
+      uint4* dst = reinterpret_cast<uint4*>(As + (size_t)buf * BM * LDK + (lrow + 128 * r) * LDK + lh * 32);
+#pragma unroll
+      for (int i = 0; i < 4; ++i) dst[i] = make_uint4(ao[r][4 * i], ao[r][4 * i + 1], ao[r][4 * i + 2], ao[r][4 * i + 3]);
+    }
+#pragma unroll
+    for (int r = 0; r < RB; ++r) {
+      uint4* dst = reinterpret_cast<uint4*>(Bs + (size_t)buf * BN * LDK + (lrow + 128 * r) * LDK + lh * 32);
+#pragma unroll
+      for (int i = 0; i < 4; ++i) dst[i] = make_uint4(wo[r][4 * i], wo[r][4 * i + 1], wo[r][4 * i + 2], wo[r][4 * i + 3]);
+    }
+  };
   auto store_lds = [&](Stage& st, int buf, int kt) {
-    if (kt * TK + TK > K) {  // uniform: the last step of a K % 64 == 32 problem
-      const bool aok = kt * TK + ah * 32 < K;
-#pragma unroll
-      for (int i = 0; i < (A32 ? 32 : 16); ++i) st.a[i] = aok ? st.a[i] : 0u;
-    }
-    uint32_t out[16];
-    if (A32) {
-#pragma unroll
-      for (int i = 0; i < 16; ++i) {
-        half2v h = {(_Float16)__builtin_bit_cast(float, st.a[2 * i]), (_Float16)__builtin_bit_cast(float, st.a[2 * i + 1])};
-        out[i] = __builtin_bit_cast(uint32_t, h);
-      }
-    } else {
-#pragma unroll
-      for (int i = 0; i < 16; ++i) out[i] = st.a[i];
-    }
-    uint4* adst = reinterpret_cast<uint4*>(As + (size_t)buf * BM * LDK + ar * LDK + ah * 32);
-#pragma unroll
-    for (int i = 0; i < 4; ++i) adst[i] = make_uint4(out[4 * i], out[4 * i + 1], out[4 * i + 2], out[4 * i + 3]);
-    const bool bok = kt * TK + bk0 < K;
-    uint32_t wq[16];
-    dequant_w<WT, AL4, BV>(st.b, bok ? bp : bp_lo, wq);
-    if (kt * TK + TK > K) {
-#pragma unroll
-      for (int i = 0; i < BV / 2; ++i) wq[i] = bok ? wq[i] : 0u;
-    }
-    _Float16* brow_p = Bs + (size_t)buf * TN * LDK + brow * LDK;
-    if (BV == 16 && WT == T0H_Q4_0) {
-      *reinterpret_cast<uint4*>(brow_p + bk0) = make_uint4(wq[0], wq[1], wq[2], wq[3]);
-      *reinterpret_cast<uint4*>(brow_p + bk0 + 16) = make_uint4(wq[4], wq[5], wq[6], wq[7]);
-    } else {
-#pragma unroll
-      for (int i = 0; i < BV / 8; ++i)
-        reinterpret_cast<uint4*>(brow_p + bk0)[i] = make_uint4(wq[4 * i], wq[4 * i + 1], wq[4 * i + 2], wq[4 * i + 3]);
-    }
+    uint32_t ao[RA][16], wo[RB][16];
+    prep(st, kt, ao, wo);
+    write(ao, wo, buf);
   };
 
-  // Each wave owns a 64x64 block as 2x2 tiles of v_mfma_f32_32x32x16_f16
-  // (measured on MI355X: this shape sustains ~2.2 PFLOP/s even at one wave per
-  // SIMD, where 16x16x32 needs 16+ independent chains and several waves).
-  // Operand lane layout: lane l holds row (A) / column (B) l%32 and k-slots
-  // (l/32)*8 .. +8 of the 16-wide K slice.
-  // B-tile rows of the wave's two column tiles; SwiGLU pairs gate tile j=0 with
-  // the up tile j=1 holding the same hidden columns.
-  int bcol[2];
+  // B-tile rows of the wave's TJ column tiles.  SwiGLU: tiles j < TJ/2 are gate
+  // columns and tile j + TJ/2 the up columns of the same hidden units.
+  int bcol[TJ];
 #pragma unroll
-  for (int j = 0; j < 2; ++j)
-    bcol[j] = EPI == EPI_SWIGLU_F16 ? j * 64 + wn * 32 : wn * 64 + j * 32;
+  for (int j = 0; j < TJ; ++j)
+    bcol[j] = SWI ? (j < TJ / 2 ? wn * (HB / 2) + j * 32 : HB + wn * (HB / 2) + (j - TJ / 2) * 32) : wn * (BN / 2) + j * 32;
 
-  floatx16 acc[2][2];
+  floatx16 acc[TI][TJ];
 #pragma unroll
-  for (int i = 0; i < 2; ++i)
+  for (int i = 0; i < TI; ++i)
 #pragma unroll
-    for (int j = 0; j < 2; ++j)
+    for (int j = 0; j < TJ; ++j)
 #pragma unroll
       for (int e = 0; e < 16; ++e) acc[i][j][e] = 0.0f;
 
-  auto compute = [&](int buf) {
-    const _Float16* At = As + (size_t)buf * BM * LDK + (wm * 64 + (lane & 31)) * LDK + (lane >> 5) * 8;
-    const _Float16* Bt = Bs + (size_t)buf * TN * LDK + (lane & 31) * LDK + (lane >> 5) * 8;
+  // Operand lane layout: lane l holds row (A) / column (B) l%32 and k-slots
+  // (l/32)*8 .. +8 of the 16-wide K slice.
+  auto compute = [&](int buf, int kk_lo = 0, int kk_hi = TK / 16) {
+    const _Float16* At = As + (size_t)buf * BM * LDK + (wm * (BM / 2) + (lane & 31)) * LDK + (lane >> 5) * 8;
+    const _Float16* Bt = Bs + (size_t)buf * BN * LDK + (lane & 31) * LDK + (lane >> 5) * 8;
+    // Fragments of slice kk+1 are read while slice kk multiplies; the
+    // scheduling fence keeps at most two slices of fragments live.
+    half8 af[2][TI], bf[2][TJ];
+    auto frags = [&](int kk, half8 (&a)[TI], half8 (&b)[TJ]) {
 #pragma unroll
-    for (int kk = 0; kk < TK / 16; ++kk) {
-      half8 af[2], bf[2];
+      for (int i = 0; i < TI; ++i) a[i] = *reinterpret_cast<const half8*>(At + i * 32 * LDK + kk * 16);
 #pragma unroll
-      for (int i = 0; i < 2; ++i) af[i] = *reinterpret_cast<const half8*>(At + i * 32 * LDK + kk * 16);
+      for (int j = 0; j < TJ; ++j) b[j] = *reinterpret_cast<const half8*>(Bt + bcol[j] * LDK + kk * 16);
+    };
+    frags(kk_lo, af[kk_lo & 1], bf[kk_lo & 1]);
+    __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
-      for (int j = 0; j < 2; ++j) bf[j] = *reinterpret_cast<const half8*>(Bt + bcol[j] * LDK + kk * 16);
+    for (int kk = kk_lo; kk < kk_hi; ++kk) {
+      if (kk + 1 < kk_hi) frags(kk + 1, af[(kk + 1) & 1], bf[(kk + 1) & 1]);
 #pragma unroll
-      for (int i = 0; i < 2; ++i)
+      for (int i = 0; i < TI; ++i)
 #pragma unroll
-        for (int j = 0; j < 2; ++j) acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(af[i], bf[j], acc[i][j], 0, 0, 0);
+        for (int j = 0; j < TJ; ++j)
+          acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(af[kk & 1][i], bf[kk & 1][j], acc[i][j], 0, 0, 0);
+      // order within the slice: the next slice's LDS reads first, then the MFMAs
+      if (kk + 1 < kk_hi) __builtin_amdgcn_sched_group_barrier(0x100, TI + TJ, 0);
+      __builtin_amdgcn_sched_group_barrier(0x008, TI * TJ, 0);
+      __builtin_amdgcn_sched_barrier(0);
     }
   };
 
-  // Steps alternate between (LDS buffer 0, stage s0) and (buffer 1, stage s1);
-  // the loop body covers two steps so the stage registers are indexed statically.
+  // One step of the two-stage pipeline in a single scheduling region: issue
+  // the loads of step kl into `ld`; multiply LDS buffer `buf`; dequantize stage
+  // `st` (step ks) with its VALU work interleaved between the MFMAs (the
+  // matrix core runs them concurrently); write it to the other buffer.
+  auto step2 = [&](int buf, Stage& ld, int kl, Stage& st) {
+    if constexpr (C::WPE == 2 && !A32 && WT != T0H_F16 && K64) {
+      constexpr int NS = TK / 16, NMS = TI * TJ, NM = NMS * NS;
+      constexpr int NCH = dq_chunks<WT>() * RB;  // dequant chunks of this thread's weight rows
+      constexpr int NW = 4 * (RA + RB);          // 16-byte LDS writes of the next step
+      load_global(ld, kl);
+      half2v dd[RB];
+#pragma unroll
+      for (int r = 0; r < RB; ++r) dd[r] = dq_scale<WT, true>(st.b[r], lh);
+      uint32_t wo[RB][16];
+      _Float16* An = As + (size_t)(buf ^ 1) * BM * LDK + lrow * LDK + lh * 32;
+      _Float16* Bn = Bs + (size_t)(buf ^ 1) * BN * LDK + lrow * LDK + lh * 32;
+      const _Float16* At = As + (size_t)buf * BM * LDK + (wm * (BM / 2) + (lane & 31)) * LDK + (lane >> 5) * 8;
+      const _Float16* Bt = Bs + (size_t)buf * BN * LDK + (lane & 31) * LDK + (lane >> 5) * 8;
+      half8 af[2][TI], bf[2][TJ];
+      auto frags = [&](int kk, half8 (&a)[TI], half8 (&b)[TJ]) {
+#pragma unroll
+        for (int i = 0; i < TI; ++i) a[i] = *reinterpret_cast<const half8*>(At + i * 32 * LDK + kk * 16);
+#pragma unroll
+        for (int j = 0; j < TJ; ++j) b[j] = *reinterpret_cast<const half8*>(Bt + bcol[j] * LDK + kk * 16);
+      };
+      frags(0, af[0], bf[0]);
+      __builtin_amdgcn_sched_barrier(0);
+      // Program order is issue order (fenced after every MFMA): each slice
+      // first reads the next slice's fragments; the dequant chunks of the next
+      // step ride behind the MFMAs of the first NS-1 slices, its LDS writes
+      // behind those of the last slice (all reads of this step are issued by
+      // then, and the writes go to the other buffer).
+#pragma unroll
+      for (int kk = 0; kk < NS; ++kk) {
+        if (kk + 1 < NS) frags(kk + 1, af[(kk + 1) & 1], bf[(kk + 1) & 1]);
+#pragma unroll
+        for (int i = 0; i < TI; ++i)
+#pragma unroll
+          for (int j = 0; j < TJ; ++j) {
+            const int mi = i * TJ + j, m = kk * NMS + mi;
+            acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(af[kk & 1][i], bf[kk & 1][j], acc[i][j], 0, 0, 0);
+#pragma unroll
+            for (int c = 0; c < NCH; ++c)
+              if (c * (NM - NMS) / NCH == m) dq_chunk<WT, true>(st.b[c / dq_chunks<WT>()], lh, c % dq_chunks<WT>(),
+                                                                 dd[c / dq_chunks<WT>()], wo[c / dq_chunks<WT>()]);
+            if (kk == NS - 1) {
+#pragma unroll
+              for (int w = 0; w < NW; ++w)
+                if (w * NMS / NW == mi) {
+                  if (w < 4 * RA) {
+                    const int r = w / 4, q = w % 4;
+                    *reinterpret_cast<uint4*>(An + 128 * r * LDK + 8 * q) =
+                        make_uint4(st.a[r][4 * q], st.a[r][4 * q + 1], st.a[r][4 * q + 2], st.a[r][4 * q + 3]);
+                  } else {
+                    const int r = (w - 4 * RA) / 4, q = (w - 4 * RA) % 4;
+                    *reinterpret_cast<uint4*>(Bn + 128 * r * LDK + 8 * q) =
+                        make_uint4(wo[r][4 * q], wo[r][4 * q + 1], wo[r][4 * q + 2], wo[r][4 * q + 3]);
+                  }
+                }
+            }
+            __builtin_amdgcn_sched_barrier(0);
+          }
+      }
+    }
+  };
+
   const int KT = (K + TK - 1) / TK;
-  Stage s0, s1;
-  load_global(s0, 0);
-  if (KT > 1) load_global(s1, 1);
-  store_lds(s0, 0, 0);
-  __syncthreads();
-  for (int kt = 0; kt < KT; kt += 2) {
-    if (kt + 2 < KT) load_global(s0, kt + 2);
-    compute(0);
-    if (kt + 1 < KT) store_lds(s1, 1, kt + 1);
+  if constexpr (C::WPE == 2 && !A32 && WT != T0H_F16 && K64) {
+    // Two register stages: steps alternate between (LDS buffer 0, stage s0) and
+    // (buffer 1, stage s1); the body covers two steps so the stage registers
+    // are indexed statically.
+    // Past the last step the loads re-read step KT-1 and the stores fill the
+    // idle buffer with it: every load and store is unconditional, so the
+    // compiler's wait counts let step kt+2's loads stay in flight.
+    Stage s0, s1;
+    const int last = KT - 1;
+    load_global(s0, 0);
+    load_global(s1, min(1, last));
+    store_lds(s0, 0, 0);
     __syncthreads();
-    if (kt + 1 >= KT) break;
-    if (kt + 3 < KT) load_global(s1, kt + 3);
-    compute(1);
-    if (kt + 2 < KT) store_lds(s0, 0, kt + 2);
+    for (int kt = 0; kt < KT; kt += 2) {
+      step2(0, s0, min(kt + 2, last), s1);
+      __syncthreads();
+      if (kt + 1 >= KT) break;
+      step2(1, s1, min(kt + 3, last), s0);
+      __syncthreads();
+    }
+  } else {
+    // One register stage: large tiles, f32 activations, f16 weights or a K tail.
+    Stage s0;
+    const int last = KT - 1;
+    load_global(s0, 0);
+    store_lds(s0, 0, 0);
     __syncthreads();
+    for (int kt = 0; kt < KT; ++kt) {
+      load_global(s0, min(kt + 1, last));
+      compute(kt & 1);
+      store_lds(s0, (kt + 1) & 1, min(kt + 1, last));
+      __syncthreads();
+    }
   }
 
   // Epilogue, staged through LDS (free after the main loop's last barrier):
@@ -377,34 +484,35 @@ __global__ __launch_bounds__(128 * NWM) __attribute__((amdgpu_waves_per_eu(2, 2)
   // f32 into its own LDS region, then streams the slice out in 16-byte row
   // chunks (coalesced f32/f16 stores, vector residual read-modify-write).
   // In each 32x32 MFMA tile lane l holds column l%32, rows (e/4)*8 + (l/32)*4 + e%4.
-  constexpr int W = EPI == EPI_SWIGLU_F16 ? 32 : 64;  // output columns per wave
-  constexpr int SLD = W + 4;                          // staging row stride (floats)
+  constexpr int W = SWI ? TJ * 16 : TJ * 32;  // output columns per wave
+  constexpr int SLD = W + 4;                  // staging row stride (floats)
+  constexpr int NJ = SWI ? TJ / 2 : TJ;       // staged 32-column groups per wave
   float* stage = reinterpret_cast<float*>(smem) + wave * 32 * SLD;
-  const int cbase = EPI == EPI_SWIGLU_F16 ? tn * 64 + wn * 32 : tn * TN + wn * 64;  // first output column
+  const int cbase = SWI ? tn * HB + wn * (HB / 2) : tn * BN + wn * (BN / 2);  // first output column
   const int lc = lane & 31, lr = (lane >> 5) * 4;
-  float bj[2];
+  float b0[NJ], b1[NJ];
 #pragma unroll
-  for (int j = 0; j < 2; ++j) {
-    const int col = EPI == EPI_SWIGLU_F16 ? cbase + lc + (j ? N : 0) : cbase + j * 32 + lc;
-    bj[j] = (d.bias && (EPI == EPI_SWIGLU_F16 ? cbase + lc < N : col < N)) ? d.bias[col] : 0.0f;
+  for (int j = 0; j < NJ; ++j) {
+    const int col = cbase + j * 32 + lc;
+    const bool ok = d.bias && col < N;
+    b0[j] = ok ? d.bias[col] : 0.0f;
+    b1[j] = (SWI && ok) ? d.bias[N + col] : 0.0f;
   }
   const bool vec_ok = (d.ldy & 3) == 0 && (N & 3) == 0;
 #pragma unroll
-  for (int i = 0; i < 2; ++i) {
+  for (int i = 0; i < TI; ++i) {
 #pragma unroll
     for (int e = 0; e < 16; ++e) {
       const int r = (e >> 2) * 8 + lr + (e & 3);
-      if (EPI == EPI_SWIGLU_F16) {
-        stage[r * SLD + lc] = silu(acc[i][0][e] + bj[0]) * (acc[i][1][e] + bj[1]);
-      } else {
-        stage[r * SLD + lc] = acc[i][0][e] + bj[0];
-        stage[r * SLD + 32 + lc] = acc[i][1][e] + bj[1];
-      }
+#pragma unroll
+      for (int j = 0; j < NJ; ++j)
+        stage[r * SLD + j * 32 + lc] =
+            SWI ? silu(acc[i][j][e] + b0[j]) * (acc[i][j + TJ / 2][e] + b1[j]) : acc[i][j][e] + b0[j];
     }
     __syncthreads();
-    const int row0 = m0 + wm * 64 + i * 32;
+    const int row0 = m0 + wm * (BM / 2) + i * 32;
 #pragma unroll
-    for (int t = 0; t < 32 * W / 4 / 64; ++t) {
+    for (int t = 0; t < W / 8; ++t) {
       const int idx = t * 64 + lane;
       const int r = idx / (W / 4), c = (idx % (W / 4)) * 4;
       const int row = row0 + r, col = cbase + c;
@@ -416,7 +524,7 @@ __global__ __launch_bounds__(128 * NWM) __attribute__((amdgpu_waves_per_eu(2, 2)
           const float4 t4 = *reinterpret_cast<const float4*>(d.row_add + (size_t)d.row_add_idx[row] * N + col);
           v.x += t4.x; v.y += t4.y; v.z += t4.z; v.w += t4.w;
         }
-        if (EPI != EPI_RESID_F32 && d.relu) {
+        if ((EPI == EPI_STORE_F32 || EPI == EPI_STORE_F16) && d.relu) {
           v.x = fmaxf(v.x, 0.0f); v.y = fmaxf(v.y, 0.0f); v.z = fmaxf(v.z, 0.0f); v.w = fmaxf(v.w, 0.0f);
         }
         if (EPI == EPI_RESID_F32) {
@@ -436,7 +544,7 @@ __global__ __launch_bounds__(128 * NWM) __attribute__((amdgpu_waves_per_eu(2, 2)
           if (col + q >= N) break;
           float x = vv[q];
           if (EPI == EPI_STORE_F32 && d.row_add) x += d.row_add[(size_t)d.row_add_idx[row] * N + col + q];
-          if (EPI != EPI_RESID_F32 && d.relu) x = fmaxf(x, 0.0f);
+          if ((EPI == EPI_STORE_F32 || EPI == EPI_STORE_F16) && d.relu) x = fmaxf(x, 0.0f);
           if (EPI == EPI_RESID_F32) {
             float* y = static_cast<float*>(d.y) + o + q;
             *y = *y + x;
@@ -448,7 +556,7 @@ __global__ __launch_bounds__(128 * NWM) __attribute__((amdgpu_waves_per_eu(2, 2)
         }
       }
     }
-    if (i == 0) __syncthreads();
+    if (i + 1 < TI) __syncthreads();
   }
 }
 
@@ -650,31 +758,35 @@ void check_hip(hipError_t e, const char* what) {
   if (e != hipSuccess) throw Error(T0H_ERR_HIP, std::string(what) + ": " + hipGetErrorString(e));
 }
 
-template <int WT, bool A32, int EPI, bool AL4, int NWM>
+template <int WT, bool A32, int EPI, bool K64, int TI, int TJ>
 void run_gemm(const GemmDesc& d, hipStream_t s) {
-  using C = TileCfg<NWM>;
-  const int tiles_n = EPI == EPI_SWIGLU_F16 ? (d.N + 63) / 64 : (d.N + TN - 1) / TN;
+  using C = Tile<TI, TJ>;
+  const int hb = EPI == EPI_SWIGLU_F16 ? C::BN / 2 : C::BN;
+  const int tiles_n = (d.N + hb - 1) / hb;
   const int tiles_m = (d.M + C::BM - 1) / C::BM;
   static bool attr_set = false;  // per instantiation
   if (!attr_set) {
-    check_hip(hipFuncSetAttribute(reinterpret_cast<const void*>(&k_gemm<WT, A32, EPI, AL4, NWM>),
+    check_hip(hipFuncSetAttribute(reinterpret_cast<const void*>(&k_gemm<WT, A32, EPI, K64, TI, TJ>),
                                   hipFuncAttributeMaxDynamicSharedMemorySize, C::LDS),
               "hipFuncSetAttribute(k_gemm)");
     attr_set = true;
   }
-  hipLaunchKernelGGL((k_gemm<WT, A32, EPI, AL4, NWM>), dim3(tiles_m * tiles_n), dim3(C::NT), C::LDS, s, d);
+  hipLaunchKernelGGL((k_gemm<WT, A32, EPI, K64, TI, TJ>), dim3(tiles_m * tiles_n), dim3(256), C::LDS, s, d);
   check_hip(hipGetLastError(), "k_gemm launch");
 }
 
-// 256-row tiles halve the dequant work per MFMA but hold one workgroup per CU,
-// so the workgroups run in lock-step; measured faster only for the f16-store
-// (QKV) shape at config-4 scale.
-template <int WT, bool A32, int EPI, bool AL4>
-void run_gemm_m(const GemmDesc& d, hipStream_t s) {
-  if (EPI == EPI_STORE_F16 && d.M > 4096)
-    run_gemm<WT, A32, EPI, AL4, 4>(d, s);
-  else
-    run_gemm<WT, A32, EPI, AL4, 2>(d, s);
+// Tile choice.  tile: 0 = by shape, 1 = 128x128, 2 = 256x128, 3 = 256x256.
+// The larger tiles are built for f16 activations with 4-byte-aligned weight
+// rows (K % 64 == 0), the shapes of the model's layers.
+template <int WT, bool A32, int EPI, bool K64>
+void run_gemm_tiled(const GemmDesc& d, int tile, hipStream_t s) {
+  if constexpr (!A32 && K64) {
+    const long cols = EPI == EPI_SWIGLU_F16 ? 2L * d.N : d.N;
+    if (tile == 0) tile = d.M >= 4096 ? (cols >= 2048 ? 3 : 2) : 1;
+    if (tile == 3) return run_gemm<WT, A32, EPI, K64, 4, 4>(d, s);
+    if (tile == 2) return run_gemm<WT, A32, EPI, K64, 4, 2>(d, s);
+  }
+  run_gemm<WT, A32, EPI, K64, 2, 2>(d, s);
 }
 
 template <int WT, bool A32, int EPI, int MT>
@@ -701,12 +813,13 @@ void dispatch_gemv(const GemmDesc& d, hipStream_t s) {
 
 template <int WT, bool A32, int EPI>
 void dispatch_w(const GemmDesc& d, int force, hipStream_t s) {
-  const bool mfma = force == 1 || (force == 0 && d.M > 16);
+  const bool mfma = force == 1 || force >= 3 || (force == 0 && d.M > 16);
   if (mfma) {
-    if (WT != T0H_F16 && d.K % 64 == 0)
-      run_gemm_m<WT, A32, EPI, true>(d, s);
+    const int tile = force >= 3 ? force - 2 : 0;
+    if (d.K % 64 == 0)
+      run_gemm_tiled<WT, A32, EPI, true>(d, tile, s);
     else
-      run_gemm_m<WT, A32, EPI, false>(d, s);
+      run_gemm_tiled<WT, A32, EPI, false>(d, tile, s);
   } else {
     dispatch_gemv<WT, A32, EPI>(d, s);
   }
