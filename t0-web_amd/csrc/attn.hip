@@ -16,6 +16,7 @@
 // its reciprocal), scores * 1/sqrt(head_dim), softmax, P*V.
 #include <hip/hip_runtime.h>
 
+#include <algorithm>
 #include <string>
 
 #include "kernels.h"
@@ -26,6 +27,7 @@ namespace {
 
 typedef _Float16 half8 __attribute__((ext_vector_type(8)));
 typedef _Float16 half4 __attribute__((ext_vector_type(4)));
+typedef _Float16 half2v __attribute__((ext_vector_type(2)));
 typedef float floatx4 __attribute__((ext_vector_type(4)));
 
 constexpr int HD = 64;
@@ -34,38 +36,55 @@ constexpr int MAXKT = T0H_MAX_PATCHES / 16;
 
 __host__ __device__ inline int round_up(int x, int m) { return (x + m - 1) / m * m; }
 
+// V^T row stride in halfs: 8-byte aligned rows (half4 operand reads) whose
+// dword stride is 2 (mod 4), so the key-pair dword writes of 8 dims x 8 key
+// pairs land in distinct banks up to a 2-way conflict.
+__host__ __device__ inline int vt_stride(int P32) { return P32 + 4; }
+
 size_t time_attn_lds(int p) {
   const int P16 = round_up(p, 16), P32 = round_up(p, 32);
-  return (size_t)(P16 + P32) * LDH * 2 + (size_t)HD * (P32 + 8) * 2 + (size_t)P32 * 4 + (size_t)P32;
+  return (size_t)(P16 + P32) * LDH * 2 + (size_t)HD * vt_stride(P32) * 2 + (size_t)P32 * 4 + (size_t)P32;
 }
 
-// One workgroup per (variate row, head); 4 waves.  Load phase: 8 lanes per
-// 64-wide q/k/v row (16 B each), QK-RMSNorm reduced over the 8-lane group,
-// interleaved xPos RoPE on the lane's 4 adjacent pairs, q/k stored row-major
-// and v transposed into LDS.  Compute phase: per 16-query tile, S^T = K Q^T
-// and O = P V on v_mfma_f32_16x16x32_f16 with the tile's scores in registers.
+
+// One workgroup per (variate row, head), 4 waves over the 16-query tiles.  Load phase: 8 lanes per 64-wide q/k row (16 B each), QK-RMSNorm
+// reduced over the 8-lane group, interleaved xPos RoPE on the lane's 4
+// adjacent pairs, q/k stored row-major; v rows in key pairs, transposed into
+// LDS as (key 2i, key 2i+1) dwords.  Compute phase: per 16-query tile,
+// S^T = K Q^T and O = P V on v_mfma_f32_16x16x32_f16 with the tile's scores in
+// registers; O is staged through the tile's own Q rows and stored in 16-byte
+// row chunks.
 template <int MAXKT>
 __global__ __launch_bounds__(256) void k_time_attn(const AttnDesc d) {
   extern __shared__ __align__(16) _Float16 sm[];
-  const int p = d.p, P16 = round_up(p, 16), P32 = round_up(p, 32), LDV = P32 + 8;
+  const int p = d.p, P16 = round_up(p, 16), P32 = round_up(p, 32), LDV = vt_stride(P32);
   _Float16* Qs = sm;
   _Float16* Ks = Qs + P16 * LDH;
   _Float16* Vt = Ks + P32 * LDH;
   int* Gk = reinterpret_cast<int*>(Vt + HD * LDV);
   uint8_t* Ak = reinterpret_cast<uint8_t*>(Gk + P32);
 
-  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6, nth = blockDim.x, nwaves = nth >> 6;
   const int r = blockIdx.x / d.heads, h = blockIdx.x % d.heads;
   const int E = d.E, ld = 3 * E;
   const size_t row0 = (size_t)r * p;
 
-  for (int i = tid; i < P32; i += 256) {
+  for (int i = tid; i < P32; i += nth) {
     Gk[i] = i < p ? d.grp[row0 + i] : -2;
     Ak[i] = i < p ? d.att[row0 + i] : 0;
   }
-  const int n_items = P16 + 2 * P32;
+  // Items: q rows, k rows, v key pairs; each 8-lane group takes every 32nd.
+  // All of a thread's global loads are issued before any is consumed.
+  const int n_items = P16 + P32 + P32 / 2;
   const int d0 = (tid & 7) * 8;
-  for (int item = tid >> 3; item < n_items; item += 32) {
+  constexpr int NIT = (MAXKT * 16 * 5 / 2 + 31) / 32;  // items per group at the largest window
+  uint4 g0[NIT], g1[NIT];
+#pragma unroll
+  for (int it = 0; it < NIT; ++it) {
+    const int item = (tid >> 3) + 32 * it;
+    g0[it] = make_uint4(0, 0, 0, 0);
+    g1[it] = make_uint4(0, 0, 0, 0);
+    if (item >= n_items) continue;
     int which, i;
     if (item < P16) {
       which = 0;
@@ -75,13 +94,36 @@ __global__ __launch_bounds__(256) void k_time_attn(const AttnDesc d) {
       i = item - P16;
     } else {
       which = 2;
-      i = item - P16 - P32;
+      i = 2 * (item - P16 - P32);
     }
-    half8 hv = {};
-    if (i < p) hv = __builtin_bit_cast(half8, *reinterpret_cast<const uint4*>(d.qkv + (row0 + i) * ld + (size_t)which * E + h * HD + d0));
-    if (which == 2) {
+    const _Float16* src = d.qkv + (row0 + i) * ld + (size_t)which * E + h * HD + d0;
+    if (i < p) g0[it] = *reinterpret_cast<const uint4*>(src);
+    if (which == 2 && i + 1 < p) g1[it] = *reinterpret_cast<const uint4*>(src + ld);
+  }
 #pragma unroll
-      for (int e = 0; e < 8; ++e) Vt[(d0 + e) * LDV + i] = hv[e];
+  for (int it = 0; it < NIT; ++it) {
+    const int item = (tid >> 3) + 32 * it;
+    if (item >= n_items) break;
+    int which, i;
+    if (item < P16) {
+      which = 0;
+      i = item;
+    } else if (item < P16 + P32) {
+      which = 1;
+      i = item - P16;
+    } else {
+      which = 2;
+      i = 2 * (item - P16 - P32);  // key pair (i, i+1)
+    }
+    const half8 hv = __builtin_bit_cast(half8, g0[it]);
+    if (which == 2) {
+      const half8 hw = __builtin_bit_cast(half8, g1[it]);
+      uint32_t* vt2 = reinterpret_cast<uint32_t*>(Vt);
+#pragma unroll
+      for (int e = 0; e < 8; ++e) {
+        const half2v pr = {hv[e], hw[e]};
+        vt2[((d0 + e) * LDV + i) >> 1] = __builtin_bit_cast(uint32_t, pr);
+      }
       continue;
     }
     float x[8];
@@ -115,7 +157,7 @@ __global__ __launch_bounds__(256) void k_time_attn(const AttnDesc d) {
 
   const bool fut = d.fut[r] != 0;
   const int nqt = P16 / 16, all_kt = P32 / 16;
-  for (int qt = wave; qt < nqt; qt += 4) {
+  for (int qt = wave; qt < nqt; qt += nwaves) {
     const int q = qt * 16 + (lane & 15);
     const int gq = q < p ? Gk[q] : -1;
     const bool need_all = fut || __ballot(q < p && gq < 0) != 0;
@@ -184,14 +226,23 @@ __global__ __launch_bounds__(256) void k_time_attn(const AttnDesc d) {
         }
       }
     }
+    // Stage O (16 queries x 64 dims) in this tile's Q rows, which only this
+    // wave reads, then write 16-byte row chunks.  LDS operations of one wave
+    // complete in order.
+    _Float16* ost = Qs + qt * 16 * LDH;
 #pragma unroll
-    for (int e = 0; e < 4; ++e) {
-      const int qrow_i = qt * 16 + (lane >> 4) * 4 + e;
-      if (qrow_i < p) {
-        _Float16* dst = d.out + (row0 + qrow_i) * E + h * HD + (lane & 15);
+    for (int e = 0; e < 4; ++e)
 #pragma unroll
-        for (int dt = 0; dt < 4; ++dt) dst[dt * 16] = (_Float16)o[dt][e];
-      }
+      for (int dt = 0; dt < 4; ++dt) ost[((lane >> 4) * 4 + e) * LDH + dt * 16 + (lane & 15)] = (_Float16)o[dt][e];
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+#pragma unroll
+    for (int c = 0; c < 2; ++c) {
+      const int rr = c * 8 + (lane >> 3), cc = (lane & 7) * 8;
+      const int qrow_i = qt * 16 + rr;
+      if (qrow_i < p)
+        *reinterpret_cast<uint4*>(d.out + (row0 + qrow_i) * E + h * HD + cc) = *reinterpret_cast<const uint4*>(ost + rr * LDH + cc);
     }
   }
 }
@@ -298,16 +349,17 @@ void launch_time_attention(const AttnDesc& d, hipStream_t s) {
     throw Error(T0H_ERR_UNSUPPORTED, "time attention: window of " + std::to_string(d.p) + " patches exceeds " +
                                          std::to_string(T0H_MAX_PATCHES));
   const size_t lds = time_attn_lds(d.p);
+  const dim3 block(256);
   if (round_up(d.p, 32) / 16 <= 8) {
     check_hip(hipFuncSetAttribute(reinterpret_cast<const void*>(&k_time_attn<8>),
                                   hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds),
               "hipFuncSetAttribute(k_time_attn)");
-    hipLaunchKernelGGL(k_time_attn<8>, dim3(d.v * d.heads), dim3(256), lds, s, d);
+    hipLaunchKernelGGL(k_time_attn<8>, dim3(d.v * d.heads), block, lds, s, d);
   } else {
     check_hip(hipFuncSetAttribute(reinterpret_cast<const void*>(&k_time_attn<MAXKT>),
                                   hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds),
               "hipFuncSetAttribute(k_time_attn)");
-    hipLaunchKernelGGL(k_time_attn<MAXKT>, dim3(d.v * d.heads), dim3(256), lds, s, d);
+    hipLaunchKernelGGL(k_time_attn<MAXKT>, dim3(d.v * d.heads), block, lds, s, d);
   }
   check_hip(hipGetLastError(), "k_time_attn launch");
 }

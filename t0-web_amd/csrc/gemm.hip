@@ -782,7 +782,7 @@ template <int WT, bool A32, int EPI, bool K64>
 void run_gemm_tiled(const GemmDesc& d, int tile, hipStream_t s) {
   if constexpr (!A32 && K64) {
     const long cols = EPI == EPI_SWIGLU_F16 ? 2L * d.N : d.N;
-    if (tile == 0) tile = d.M >= 4096 ? (cols >= 2048 ? 3 : 2) : 1;
+    if (tile == 0) tile = d.M >= 4096 && cols >= 2048 ? 3 : 1;  // 256x128 measured slower at every shape
     if (tile == 3) return run_gemm<WT, A32, EPI, K64, 4, 4>(d, s);
     if (tile == 2) return run_gemm<WT, A32, EPI, K64, 4, 2>(d, s);
   }
