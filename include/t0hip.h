@@ -173,6 +173,16 @@ int t0h_dequant(int qtype, const void* d_blocks, size_t n_elements, float* d_out
  * W is [n, k] in GGUF layout of `wtype` (F16, Q8_0, Q4_0).  f32 in, f32 out. */
 int t0h_gemm_q(int wtype, const void* d_w, const float* d_x, const float* d_bias, float* d_y, size_t m, size_t n,
                size_t k, int act, void* stream);
+/* The forward's own GEMM kernels (f16 activations), exposed for kernel-level
+ * parity tests and benchmarks.  d_x: f16 [m, k]; d_y: per epilogue
+ *   0: f32 [m, n] = x W^T + b;  1: f16 [m, n] = x W^T + b;
+ *   2: f32 [m, n] += x W^T + b (residual stream, model.rs:782-786);
+ *   3: f16 [m, n] = silu(x W_g^T + b_g) * (x W_u^T + b_u), W with 2n rows gate
+ *      first (ops.rs:57-61) — the fused SwiGLU of the FFN.
+ * tile: 0 = as the forward picks, 1 = 128x128, 3 = 256x256, 4 = 256x256 with
+ * DMA-fed activations (K % 128 == 0, quantized weights; falls back to 1). */
+int t0h_gemm_f16(int wtype, const void* d_w, const void* d_x, const float* d_bias, void* d_y, size_t m, size_t n,
+                 size_t k, int epilogue, int tile, void* stream);
 
 /* ---- host codec, export, synthetic model -------------------------------- */
 /* GgmlType::row_bytes (gguf.rs:61-70); 0 for an invalid count. */

@@ -561,6 +561,253 @@ void k_gemm(const GemmDesc d) {
 }
 
 // ---------------------------------------------------------------------------
+// DMA tile kernel: 256x256x64 tiles for K % 64 == 0, f16 activations and
+// Q8_0/Q4_0 weights (the model's layer shapes).  Four waves, each 128x128 as
+// 4x4 tiles of v_mfma_f32_32x32x16_f16 with the 256 accumulators in AGPRs.
+//  * Activation tiles go global -> LDS with global_load_lds_dwordx4 (no
+//    registers, tracked by vmcnt), three buffers deep: step kt+2 is in flight
+//    while kt multiplies.
+//  * Weight blocks go global -> registers one step ahead, are dequantized in
+//    chunks between the MFMAs of the current step and written as f16 to the
+//    other of two weight buffers.
+//  * LDS rows are 128 bytes, unpadded, with 16-byte chunk c of row r stored in
+//    slot c ^ ((r >> 1) & 7): the DMA writes (8 rows per wave instruction), the
+//    weight writes and the 32x32 operand reads are all free of bank conflicts.
+// ---------------------------------------------------------------------------
+constexpr int DM_BM = 256, DM_BN = 256, DM_ROWB = 128;  // tile rows / cols, LDS row bytes
+constexpr int DM_ABUF = DM_BM * DM_ROWB, DM_BBUF = DM_BN * DM_ROWB;
+constexpr int DM_LDS = 3 * DM_ABUF + 2 * DM_BBUF;  // 160 KiB
+
+__device__ __forceinline__ int dm_slot(int row, int chunk) { return chunk ^ ((row >> 1) & 7); }
+
+template <int WT, int EPI>
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1))) void k_gemm_dma(const GemmDesc d) {
+  constexpr int TI = 4, TJ = 4, RB = 2;
+  constexpr bool SWI = EPI == EPI_SWIGLU_F16;
+  constexpr int HB = SWI ? DM_BN / 2 : DM_BN;
+  extern __shared__ __align__(16) _Float16 smem[];
+  char* const lds = reinterpret_cast<char*>(smem);
+
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int wm = wave >> 1, wn = wave & 1;
+  const int M = d.M, N = d.N, K = d.K;
+  const int tiles_n = (N + HB - 1) / HB;
+  const int total = gridDim.x, bid = blockIdx.x;
+  const int per = total / 8;
+  const int logical = bid < per * 8 ? (bid % 8) * per + bid / 8 : bid;
+  const int tm = logical / tiles_n, tn = logical % tiles_n;
+  const int m0 = tm * DM_BM;
+  const int KT = K / TK, last = KT - 1;
+
+  // Activation DMA: wave w fills rows w*64 .. w*64+63 with 8 instructions of
+  // 8 rows each; lane L writes slot L%8 of row +L/8, so it fetches chunk
+  // (L%8) ^ swizzle(row).  Rows past M read row M-1.
+  const char* asrc[8];
+#pragma unroll
+  for (int q = 0; q < 8; ++q) {
+    const int row = wave * 64 + q * 8 + (lane >> 3);
+    const int chunk = (lane & 7) ^ ((row >> 1) & 7);
+    asrc[q] = static_cast<const char*>(d.a) + (size_t)min(m0 + row, M - 1) * d.lda * 2 + chunk * 16;
+  }
+  auto dma_a = [&](int kt, int buf) {
+    char* dst = lds + buf * DM_ABUF + wave * 64 * DM_ROWB;
+#pragma unroll
+    for (int q = 0; q < 8; ++q)
+      __builtin_amdgcn_global_load_lds(asrc[q] + kt * (TK * 2), dst + q * 8 * DM_ROWB, 16, 0, 0);
+  };
+
+  // Weight rows: thread t moves tile rows t/2 and t/2+128, block t%2 of each step.
+  const int lrow = tid >> 1, lh = tid & 1;
+  const size_t rowb = (size_t)(K / 32) * block_bytes(WT);
+  const uint8_t* wbase[RB];
+#pragma unroll
+  for (int r = 0; r < RB; ++r) {
+    const int br = lrow + 128 * r;
+    int wrow;
+    bool ok;
+    if (SWI) {
+      const int g = tn * HB + (br % HB);
+      ok = g < N;
+      wrow = br < HB ? g : N + g;
+    } else {
+      wrow = tn * DM_BN + br;
+      ok = wrow < N;
+    }
+    wbase[r] = static_cast<const uint8_t*>(d.w) + (size_t)(ok ? wrow : 0) * rowb;
+  }
+  struct WStage {
+    uint32_t b[RB][16];
+  };
+  auto load_b = [&](WStage& st, int kt) {
+#pragma unroll
+    for (int r = 0; r < RB; ++r) load_w<WT, true>(wbase[r], kt, lh, st.b[r]);
+  };
+  auto write_b_chunk = [&](const uint32_t (&wo)[16], int r, int q, int buf) {
+    const int br = lrow + 128 * r;
+    *reinterpret_cast<uint4*>(lds + 3 * DM_ABUF + buf * DM_BBUF + br * DM_ROWB + dm_slot(br, lh * 4 + q) * 16) =
+        make_uint4(wo[4 * q], wo[4 * q + 1], wo[4 * q + 2], wo[4 * q + 3]);
+  };
+
+  int bcol[TJ];
+#pragma unroll
+  for (int j = 0; j < TJ; ++j)
+    bcol[j] = SWI ? (j < TJ / 2 ? wn * (HB / 2) + j * 32 : HB + wn * (HB / 2) + (j - TJ / 2) * 32) : wn * (DM_BN / 2) + j * 32;
+
+  floatx16 acc[TI][TJ];
+#pragma unroll
+  for (int i = 0; i < TI; ++i)
+#pragma unroll
+    for (int j = 0; j < TJ; ++j)
+#pragma unroll
+      for (int e = 0; e < 16; ++e) acc[i][j][e] = 0.0f;
+
+  // Operand reads: lane l takes row l%32 of each 32-row tile and 16-byte chunk
+  // 2*kk + l/32; every tile row base is a multiple of 32, so the swizzle of the
+  // lane's row is ((l%32) >> 1) & 7 throughout.
+  const int swz = ((lane & 31) >> 1) & 7;
+  int koff[TK / 16];
+#pragma unroll
+  for (int kk = 0; kk < TK / 16; ++kk) koff[kk] = (((2 * kk + (lane >> 5)) ^ swz) * 16);
+  const int arow = (wm * (DM_BM / 2) + (lane & 31)) * DM_ROWB, brow = (lane & 31) * DM_ROWB;
+
+  // Prologue: A(0), B(0) and A(1), B(1) in flight; B(0) dequantized into buffer 0.
+  WStage w0, w1;
+  dma_a(0, 0);
+  load_b(w0, 0);
+  dma_a(min(1, last), 1);
+  load_b(w1, min(1, last));
+  {
+    uint32_t wo[RB][16];
+#pragma unroll
+    for (int r = 0; r < RB; ++r) dequant_w<WT, true>(w0.b[r], lh, wo[r]);
+#pragma unroll
+    for (int r = 0; r < RB; ++r)
+#pragma unroll
+      for (int q = 0; q < 4; ++q) write_b_chunk(wo[r], r, q, 0);
+  }
+  // A(0) landed: its DMA precedes B(1)'s loads, which dequant_w above did not
+  // wait for; wait for everything but the step-1 loads.
+  __builtin_amdgcn_s_waitcnt((8 + RB * (WT == T0H_Q8_0 ? 3 : 2)) | (7 << 4) | (15 << 8));
+  __syncthreads();
+
+  // One step: DMA A(kt+2), load B(kt+2); multiply buffers (kt%3, kt&1);
+  // dequantize B(kt+1) between the MFMAs and write it to buffer (kt+1)&1.
+  auto step = [&](int kt, int abuf, WStage& cur, WStage& nxt) {
+    constexpr int NS = TK / 16, NMS = TI * TJ, NM = NMS * NS;
+    constexpr int NCHR = dq_chunks<WT>(), NCH = NCHR * RB;
+    dma_a(min(kt + 2, last), (abuf + 2) % 3);
+    load_b(nxt, min(kt + 2, last));
+    half2v dd[RB];
+#pragma unroll
+    for (int r = 0; r < RB; ++r) dd[r] = dq_scale<WT, true>(cur.b[r], lh);
+    uint32_t wo[RB][16];
+    const char* At = lds + abuf * DM_ABUF + arow;
+    const char* Bt = lds + 3 * DM_ABUF + (kt & 1) * DM_BBUF + brow;
+    half8 af[2][TI], bf[2][TJ];
+    auto frags = [&](int kk, half8 (&a)[TI], half8 (&b)[TJ]) {
+#pragma unroll
+      for (int i = 0; i < TI; ++i) a[i] = *reinterpret_cast<const half8*>(At + i * 32 * DM_ROWB + koff[kk]);
+#pragma unroll
+      for (int j = 0; j < TJ; ++j) b[j] = *reinterpret_cast<const half8*>(Bt + bcol[j] * DM_ROWB + koff[kk]);
+    };
+    frags(0, af[0], bf[0]);
+    __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+    for (int kk = 0; kk < NS; ++kk) {
+      if (kk + 1 < NS) frags(kk + 1, af[(kk + 1) & 1], bf[(kk + 1) & 1]);
+#pragma unroll
+      for (int i = 0; i < TI; ++i)
+#pragma unroll
+        for (int j = 0; j < TJ; ++j) {
+          const int mi = i * TJ + j, m = kk * NMS + mi;
+          acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(af[kk & 1][i], bf[kk & 1][j], acc[i][j], 0, 0, 0);
+#pragma unroll
+          for (int c = 0; c < NCH; ++c)
+            if (c * (NM - NMS) / NCH == m) dq_chunk<WT, true>(cur.b[c / NCHR], lh, c % NCHR, dd[c / NCHR], wo[c / NCHR]);
+          if (kk == NS - 1) {
+#pragma unroll
+            for (int w = 0; w < 4 * RB; ++w)
+              if (w * NMS / (4 * RB) == mi) write_b_chunk(wo[w / 4], w / 4, w % 4, (kt + 1) & 1);
+          }
+          __builtin_amdgcn_sched_barrier(0);
+        }
+    }
+    // A(kt+1) landed (issued before B(kt+1), whose data the dequant consumed).
+    __builtin_amdgcn_s_waitcnt((8 + RB * (WT == T0H_Q8_0 ? 3 : 2)) | (7 << 4) | (15 << 8));
+    __syncthreads();
+  };
+
+  // KT is even (checked at launch): two steps per iteration, one loop exit.
+  int abuf = 0;
+  for (int kt = 0; kt < KT; kt += 2) {
+    step(kt, abuf, w1, w0);
+    abuf = abuf == 2 ? 0 : abuf + 1;
+    step(kt + 1, abuf, w0, w1);
+    abuf = abuf == 2 ? 0 : abuf + 1;
+  }
+
+  // The last steps re-issued DMA into idle buffers; all of it must land before
+  // the epilogue reuses the LDS.
+  __builtin_amdgcn_s_waitcnt(0 | (7 << 4) | (15 << 8));
+  __syncthreads();
+
+  // Epilogue (as k_gemm): per-wave 32-row slices staged in LDS as f32.
+  constexpr int W = SWI ? TJ * 16 : TJ * 32;
+  constexpr int SLD = W + 4;
+  constexpr int NJ = SWI ? TJ / 2 : TJ;
+  float* stage = reinterpret_cast<float*>(smem) + wave * 32 * SLD;
+  const int cbase = SWI ? tn * HB + wn * (HB / 2) : tn * DM_BN + wn * (DM_BN / 2);
+  const int lc = lane & 31, lr = (lane >> 5) * 4;
+  float b0[NJ], b1[NJ];
+#pragma unroll
+  for (int j = 0; j < NJ; ++j) {
+    const int col = cbase + j * 32 + lc;
+    const bool ok = d.bias && col < N;
+    b0[j] = ok ? d.bias[col] : 0.0f;
+    b1[j] = (SWI && ok) ? d.bias[N + col] : 0.0f;
+  }
+#pragma unroll
+  for (int i = 0; i < TI; ++i) {
+#pragma unroll
+    for (int e = 0; e < 16; ++e) {
+      const int r = (e >> 2) * 8 + lr + (e & 3);
+#pragma unroll
+      for (int j = 0; j < NJ; ++j)
+        stage[r * SLD + j * 32 + lc] =
+            SWI ? silu(acc[i][j][e] + b0[j]) * (acc[i][j + TJ / 2][e] + b1[j]) : acc[i][j][e] + b0[j];
+    }
+    __syncthreads();
+    const int row0 = m0 + wm * (DM_BM / 2) + i * 32;
+#pragma unroll
+    for (int t = 0; t < W / 8; ++t) {
+      const int idx = t * 64 + lane;
+      const int r = idx / (W / 4), c = (idx % (W / 4)) * 4;
+      const int row = row0 + r, col = cbase + c;
+      if (row >= M || col >= N) continue;
+      float4 v = *reinterpret_cast<const float4*>(stage + r * SLD + c);
+      const size_t o = (size_t)row * d.ldy + col;
+      if (EPI == EPI_RESID_F32) {
+        float4* y = reinterpret_cast<float4*>(static_cast<float*>(d.y) + o);
+        const float4 old = *y;
+        *y = make_float4(old.x + v.x, old.y + v.y, old.z + v.z, old.w + v.w);
+      } else if (EPI == EPI_STORE_F32) {
+        if (d.row_add) {
+          const float4 t4 = *reinterpret_cast<const float4*>(d.row_add + (size_t)d.row_add_idx[row] * N + col);
+          v.x += t4.x; v.y += t4.y; v.z += t4.z; v.w += t4.w;
+        }
+        if (d.relu) { v.x = fmaxf(v.x, 0.0f); v.y = fmaxf(v.y, 0.0f); v.z = fmaxf(v.z, 0.0f); v.w = fmaxf(v.w, 0.0f); }
+        *reinterpret_cast<float4*>(static_cast<float*>(d.y) + o) = v;
+      } else {
+        if (EPI == EPI_STORE_F16 && d.relu) { v.x = fmaxf(v.x, 0.0f); v.y = fmaxf(v.y, 0.0f); v.z = fmaxf(v.z, 0.0f); v.w = fmaxf(v.w, 0.0f); }
+        half4 h = {(_Float16)v.x, (_Float16)v.y, (_Float16)v.z, (_Float16)v.w};
+        *reinterpret_cast<half4*>(static_cast<_Float16*>(d.y) + o) = h;
+      }
+    }
+    if (i + 1 < TI) __syncthreads();
+  }
+}
+
+// ---------------------------------------------------------------------------
 // Small-M kernel: 16 weight rows per workgroup staged in LDS, exact f32 math.
 // ---------------------------------------------------------------------------
 constexpr int GV_NR = 16;
@@ -778,11 +1025,36 @@ void run_gemm(const GemmDesc& d, hipStream_t s) {
 // Tile choice.  tile: 0 = by shape, 1 = 128x128, 2 = 256x128, 3 = 256x256.
 // The larger tiles are built for f16 activations with 4-byte-aligned weight
 // rows (K % 64 == 0), the shapes of the model's layers.
+// The DMA kernel needs an even number of 64-wide K steps and output rows
+// that take 16-byte (f32) / 8-byte (f16) vector stores.
+bool dma_ok(const GemmDesc& d) { return d.K % 128 == 0 && d.N % 4 == 0 && d.ldy % 4 == 0; }
+
+template <int WT, int EPI>
+void run_gemm_dma(const GemmDesc& d, hipStream_t s) {
+  const int hb = EPI == EPI_SWIGLU_F16 ? DM_BN / 2 : DM_BN;
+  const int tiles_n = (d.N + hb - 1) / hb;
+  const int tiles_m = (d.M + DM_BM - 1) / DM_BM;
+  static bool attr_set = false;
+  if (!attr_set) {
+    check_hip(hipFuncSetAttribute(reinterpret_cast<const void*>(&k_gemm_dma<WT, EPI>),
+                                  hipFuncAttributeMaxDynamicSharedMemorySize, DM_LDS),
+              "hipFuncSetAttribute(k_gemm_dma)");
+    attr_set = true;
+  }
+  hipLaunchKernelGGL((k_gemm_dma<WT, EPI>), dim3(tiles_m * tiles_n), dim3(256), DM_LDS, s, d);
+  check_hip(hipGetLastError(), "k_gemm_dma launch");
+}
+
 template <int WT, bool A32, int EPI, bool K64>
 void run_gemm_tiled(const GemmDesc& d, int tile, hipStream_t s) {
+  if constexpr (!A32 && K64 && WT != T0H_F16) {
+    if (tile == 4 && dma_ok(d)) return run_gemm_dma<WT, EPI>(d, s);
+  }
   if constexpr (!A32 && K64) {
     const long cols = EPI == EPI_SWIGLU_F16 ? 2L * d.N : d.N;
-    if (tile == 0) tile = d.M >= 4096 && cols >= 2048 ? 3 : 1;  // 256x128 measured slower at every shape
+    // Measured at the model's shapes: 256x256 DMA-fed tiles for wide outputs
+    // (QKV, SwiGLU), 128x128 for N = 768; 256x128 was slower everywhere.
+    if (tile == 0) tile = d.M >= 4096 && cols >= 2048 ? (dma_ok(d) && WT != T0H_F16 ? 4 : 3) : 1;
     if (tile == 3) return run_gemm<WT, A32, EPI, K64, 4, 4>(d, s);
     if (tile == 2) return run_gemm<WT, A32, EPI, K64, 4, 2>(d, s);
   }

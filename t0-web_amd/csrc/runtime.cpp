@@ -1212,6 +1212,29 @@ int t0h_gemm_q(int wtype, const void* d_w, const float* d_x, const float* d_bias
   API_END
 }
 
+int t0h_gemm_f16(int wtype, const void* d_w, const void* d_x, const float* d_bias, void* d_y, size_t m, size_t n,
+                 size_t k, int epilogue, int tile, void* stream) {
+  API_BEGIN
+  require(m < (1u << 31) && n < (1u << 31) && k < (1u << 31), "t0h_gemm_f16: dimension too large");
+  require(epilogue >= EPI_STORE_F32 && epilogue <= EPI_SWIGLU_F16, "t0h_gemm_f16: unknown epilogue");
+  require(tile >= 0 && tile <= 4 && tile != 2, "t0h_gemm_f16: tile must be 0, 1, 3 or 4");
+  GemmDesc d;
+  d.wtype = wtype;
+  d.w = d_w;
+  d.a = d_x;
+  d.a_f32 = 0;
+  d.lda = (int)k;
+  d.bias = d_bias;
+  d.y = d_y;
+  d.ldy = (int)n;
+  d.M = (int)m;
+  d.N = (int)n;
+  d.K = (int)k;
+  d.epi = epilogue;
+  launch_gemm_forced(d, tile == 0 ? 0 : tile + 2, static_cast<hipStream_t>(stream));
+  API_END
+}
+
 size_t t0h_row_bytes(int qtype, size_t n) { return row_bytes(qtype, n); }
 
 int t0h_quantize(int qtype, const float* x, size_t n, uint8_t* out, size_t out_len) {

@@ -75,7 +75,7 @@ SYMBOLS = [
     "t0h_model_load_gguf", "t0h_model_destroy", "t0h_model_config", "t0h_model_weight_bytes", "t0h_model_stream",
     "t0h_model_workspace", "t0h_model_profile", "t0h_model_profile_entry", "t0h_forward", "t0h_forecast", "t0h_forecast_batch_chunked",
     "t0h_forecast_batch_rows_chunked", "t0h_forecast_grouped", "t0h_forecast_grouped_dev",
-    "t0h_forecast_grouped_ar", "t0h_forecast_rollout", "t0h_dequant", "t0h_gemm_q", "t0h_row_bytes",
+    "t0h_forecast_grouped_ar", "t0h_forecast_rollout", "t0h_dequant", "t0h_gemm_q", "t0h_gemm_f16", "t0h_row_bytes",
     "t0h_quantize", "t0h_synth_model_gguf", "t0h_export_gguf",
 ]
 
@@ -116,6 +116,7 @@ def lib():
     L.t0h_forecast_rollout.argtypes = [P, P, S, S, P, S, P, S]
     L.t0h_dequant.argtypes = [I, P, S, P, P]
     L.t0h_gemm_q.argtypes = [I, P, P, P, P, S, S, S, I, P]
+    L.t0h_gemm_f16.argtypes = [I, P, P, P, P, S, S, S, I, I, P]
     L.t0h_row_bytes.restype = S
     L.t0h_row_bytes.argtypes = [I, S]
     L.t0h_quantize.argtypes = [I, P, S, P, S]
@@ -379,3 +380,12 @@ def dequant_dev(qtype, d_blocks, n, d_out, stream=None):
 def gemm_q_dev(wtype, d_w, d_x, d_bias, d_y, m, n, k, act=0, stream=None):
     _check(lib().t0h_gemm_q(wtype, C.c_void_p(d_w), C.c_void_p(d_x), C.c_void_p(d_bias) if d_bias else None,
                             C.c_void_p(d_y), m, n, k, act, C.c_void_p(stream)))
+
+
+EPI_STORE_F32, EPI_STORE_F16, EPI_RESID_F32, EPI_SWIGLU_F16 = 0, 1, 2, 3
+
+
+def gemm_f16_dev(wtype, d_w, d_x, d_bias, d_y, m, n, k, epilogue, tile=0, stream=None):
+    """The forward's GEMM kernels on device pointers: f16 x [m, k]; see t0hip.h t0h_gemm_f16."""
+    _check(lib().t0h_gemm_f16(wtype, C.c_void_p(d_w), C.c_void_p(d_x), C.c_void_p(d_bias) if d_bias else None,
+                              C.c_void_p(d_y), m, n, k, epilogue, tile, C.c_void_p(stream)))

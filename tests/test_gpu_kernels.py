@@ -136,3 +136,46 @@ def test_gemm_linearity_and_zero_weights(torch_cuda, t0hip, oracle, rng):
     y1 = run_gemm(torch_cuda, t0hip, 2, W, x, None, n)
     y2 = run_gemm(torch_cuda, t0hip, 2, W, 2 * x, None, n)
     assert np.array_equal(2 * y1, y2)
+
+
+# The forward's GEMM paths (f16 activations, fused epilogues) at model shapes,
+# M ragged against every tile height: (k, n) per epilogue as in the layer
+# (wO store, QKV f16, w2 residual, w0 SwiGLU with n hidden units).
+FWD_SHAPES = {0: (768, 768), 1: (768, 2304), 2: (2048, 768), 3: (768, 2048)}
+
+
+@pytest.mark.parametrize("qtype", [8, 2])
+@pytest.mark.parametrize("tile", [1, 3, 4])
+@pytest.mark.parametrize("epi", [0, 1, 2, 3])
+def test_forward_gemm_paths(torch_cuda, t0hip, oracle, rng, qtype, tile, epi):
+    """linear() (model.rs:406-504) as the forward runs it: f16 x, f32 accumulation,
+    epilogues bias / f16 store / residual add / SwiGLU (ops.rs:49-62); 1e-2 relative
+    on a 512-row sample of M = 4192 rows."""
+    torch = torch_cuda
+    k, n = FWD_SHAPES[epi]
+    m = 4192
+    wrows = 2 * n if epi == 3 else n
+    W = (0.02 * rng.standard_normal((wrows, k))).astype(np.float32)
+    b = (0.02 * rng.standard_normal(wrows)).astype(np.float32)
+    x16 = rng.standard_normal((m, k)).astype(np.float16)
+    blocks = oracle.quantize(qtype, W)
+    deq = oracle.dequantize(qtype, blocks, wrows * k).reshape(wrows, k).astype(np.float64)
+    d_w, d_x, d_b = dev(torch, blocks), dev(torch, x16), dev(torch, b)
+    out_dtype = torch.float16 if epi in (1, 3) else torch.float32
+    y0 = rng.standard_normal((m, n)).astype(np.float32)
+    d_y = dev(torch, y0) if epi == 2 else torch.empty((m, n), dtype=out_dtype, device="cuda")
+    t0hip.gemm_f16_dev(qtype, d_w.data_ptr(), d_x.data_ptr(), d_b.data_ptr(), d_y.data_ptr(), m, n, k, epi, tile,
+                       torch.cuda.current_stream().cuda_stream)
+    torch.cuda.synchronize()
+    got = d_y.float().cpu().numpy()
+    rows = np.sort(np.concatenate([rng.choice(m - 200, 312, replace=False), np.arange(m - 200, m)]))
+    h = x16[rows].astype(np.float64) @ deq.T + b
+    if epi == 3:
+        g, u = h[:, :n], h[:, n:]
+        want = g / (1.0 + np.exp(-g)) * u
+    elif epi == 2:
+        want = y0[rows] + h
+    else:
+        want = h
+    e = rel_err(got[rows], want)
+    assert e < 1e-2, e
