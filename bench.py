@@ -146,10 +146,11 @@ def cpu_baseline(gguf, x, groups, t_ctx, horizon, budget_s=12.0):
                       f"{dt:.1f} s"}
 
 
-# Device kernel behind each profiled GEMM kind of the forward (template args:
-# weight type 2 = Q4_0 / 8 = Q8_0, f32 activations, epilogue 1 f16 store / 3 SwiGLU).
-KERNEL_OF = {("gemm_w0_swiglu", "q4_0"): "k_gemm<2, false, 3,", ("gemm_w0_swiglu", "q8_0"): "k_gemm<8, false, 3,",
-             ("gemm_qkv", "q4_0"): "k_gemm<2, false, 1,", ("gemm_qkv", "q8_0"): "k_gemm<8, false, 1,"}
+# Device kernel behind each profiled GEMM kind of the forward at config 4
+# (template args: weight type 2 = Q4_0 / 8 = Q8_0, epilogue 1 f16 store / 3 SwiGLU).
+KERNEL_OF = {("gemm_w0_swiglu", "q4_0"): "k_gemm<2, false, 3, true, 2, 2>",
+             ("gemm_w0_swiglu", "q8_0"): "k_gemm<8, false, 3, true, 2, 2>",
+             ("gemm_qkv", "q4_0"): "k_gemm<2, false, 1, true, 2, 2>", ("gemm_qkv", "q8_0"): "k_gemm<8, false, 1, true, 2, 2>"}
 COPY_BYTES = 256 << 20  # the --calibrate-copy kernel reads and writes this many bytes
 TRAFFIC_FILE = os.path.join(ROOT, "profiles", "traffic_config4.json")
 
@@ -205,7 +206,7 @@ def summarize(prof_dir, fetch_dir, write_dir, quant, kind):
         res[ctr.lower()] = {"kib_per_dispatch_raw": round(sum(vals) / len(vals), 1), "copy_factor": round(factor, 3),
                             "bytes_per_launch": int(per), "dispatches": len(vals)}
     res["traffic"] = res["fetch_size"]["bytes_per_launch"] + res["write_size"]["bytes_per_launch"]
-    lines += ["", f"HBM traffic of `{KERNEL_OF[(kind, quant)]} ...>` ({kind}, {quant}) per launch:",
+    lines += ["", f"HBM traffic of `{KERNEL_OF[(kind, quant)]}` ({kind}, {quant}) per launch:",
               f"FETCH_SIZE {res['fetch_size']['kib_per_dispatch_raw']} KiB x {res['fetch_size']['copy_factor']} "
               f"+ WRITE_SIZE {res['write_size']['kib_per_dispatch_raw']} KiB x {res['write_size']['copy_factor']} "
               f"= {res['traffic'] / 1e6:.1f} MB"]

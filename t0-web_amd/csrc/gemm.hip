@@ -1047,15 +1047,15 @@ void run_gemm_dma(const GemmDesc& d, hipStream_t s) {
 
 template <int WT, bool A32, int EPI, bool K64>
 void run_gemm_tiled(const GemmDesc& d, int tile, hipStream_t s) {
+  // By shape (tile 0): 128x128 everywhere.  Measured in the config-4 forward,
+  // 128x128 at two workgroups per CU beat the 256x256 tiles (one workgroup per
+  // CU, DMA-fed or not) and 256x128 at every layer shape.
+  if (tile == 0) tile = 1;
   if constexpr (!A32 && K64 && WT != T0H_F16) {
     if (tile == 4 && dma_ok(d)) return run_gemm_dma<WT, EPI>(d, s);
   }
   if constexpr (!A32 && K64) {
-    const long cols = EPI == EPI_SWIGLU_F16 ? 2L * d.N : d.N;
-    // Measured at the model's shapes: 256x256 DMA-fed tiles for wide outputs
-    // (QKV, SwiGLU), 128x128 for N = 768; 256x128 was slower everywhere.
-    if (tile == 0) tile = d.M >= 4096 && cols >= 2048 ? (dma_ok(d) && WT != T0H_F16 ? 4 : 3) : 1;
-    if (tile == 3) return run_gemm<WT, A32, EPI, K64, 4, 4>(d, s);
+    if (tile == 3 || tile == 4) return run_gemm<WT, A32, EPI, K64, 4, 4>(d, s);
     if (tile == 2) return run_gemm<WT, A32, EPI, K64, 4, 2>(d, s);
   }
   run_gemm<WT, A32, EPI, K64, 2, 2>(d, s);
