@@ -247,85 +247,90 @@ __global__ __launch_bounds__(256) void k_time_attn(const AttnDesc d) {
   }
 }
 
-// Group attention: one thread per (query row, head), keys restricted to the
-// query row's group (segment of a group-sorted permutation); online softmax.
+// Group attention: 8 lanes per (query row, head), each lane owning 8 of the
+// 64 dims; a wave covers 8 consecutive heads of a row, so every q/k/v load is
+// one contiguous 1 KB span.  Keys are the query row's group (a segment of the
+// group-sorted permutation); the norms and dot products reduce over the 8-lane
+// group with xor-shuffles; online softmax.
+__device__ __forceinline__ float sum8(float x) {
+  x += __shfl_xor(x, 1);
+  x += __shfl_xor(x, 2);
+  x += __shfl_xor(x, 4);
+  return x;
+}
+
 __global__ __launch_bounds__(256) void k_group_attn(const AttnDesc d) {
   const int H = d.heads, E = d.E, p = d.p, v = d.v, ld = 3 * E;
-  const long long task = (long long)blockIdx.x * 256 + threadIdx.x;
-  if (task >= (long long)v * p * H) return;
+  const long long task = ((long long)blockIdx.x * 256 + threadIdx.x) >> 3;
+  const int sub = threadIdx.x & 7, d0 = sub * 8;
+  if (task >= (long long)v * p * H) return;  // whole 8-lane groups exit together
   const int h = (int)(task % H);
   const long long m = task / H;
   const int r = (int)(m / p), pi = (int)(m % p);
   const int gq = d.grp[m];
-  float o[HD];
+  auto ld8 = [&](long long row, int which, float (&x)[8]) {
+    const half8 hv = __builtin_bit_cast(half8, *reinterpret_cast<const uint4*>(d.qkv + row * ld + (size_t)which * E + h * HD + d0));
 #pragma unroll
-  for (int dd = 0; dd < HD; ++dd) o[dd] = 0.0f;
-
-  auto load = [&](long long row, int which, float (&x)[HD]) {
-    const uint4* src = reinterpret_cast<const uint4*>(d.qkv + row * ld + (size_t)which * E + h * HD);
-#pragma unroll
-    for (int c = 0; c < 8; ++c) {
-      const half8 hv = __builtin_bit_cast(half8, src[c]);
-#pragma unroll
-      for (int e = 0; e < 8; ++e) x[c * 8 + e] = (float)hv[e];
-    }
+    for (int e = 0; e < 8; ++e) x[e] = (float)hv[e];
   };
-
-  if (gq < 0) {
-    float vv[HD];
-    for (int j = 0; j < v; ++j) {
-      load((long long)j * p + pi, 2, vv);
+  float o[8];
 #pragma unroll
-      for (int dd = 0; dd < HD; ++dd) o[dd] += vv[dd];
+  for (int e = 0; e < 8; ++e) o[e] = 0.0f;
+
+  if (gq < 0) {  // all-PAD patch: every score is -1e9, uniform weights over all v rows
+    for (int j = 0; j < v; ++j) {
+      float vv[8];
+      ld8((long long)j * p + pi, 2, vv);
+#pragma unroll
+      for (int e = 0; e < 8; ++e) o[e] += vv[e];
     }
     const float inv = 1.0f / (float)v;
 #pragma unroll
-    for (int dd = 0; dd < HD; ++dd) o[dd] *= inv;
+    for (int e = 0; e < 8; ++e) o[e] *= inv;
   } else {
-    float qn[HD];
-    load(m, 0, qn);
+    float qn[8], kn[8];
+    ld8(m, 0, qn);
+#pragma unroll
+    for (int e = 0; e < 8; ++e) kn[e] = d.k_norm[d0 + e];
     float ss = 0.0f;
 #pragma unroll
-    for (int dd = 0; dd < HD; ++dd) ss += qn[dd] * qn[dd];
-    const float dq = sqrtf(ss / (float)HD + 1e-8f);
+    for (int e = 0; e < 8; ++e) ss += qn[e] * qn[e];
+    const float dq = sqrtf(sum8(ss) / (float)HD + 1e-8f);
 #pragma unroll
-    for (int dd = 0; dd < HD; ++dd) qn[dd] = (qn[dd] / dq) * d.q_norm[dd];
+    for (int e = 0; e < 8; ++e) qn[e] = (qn[e] / dq) * d.q_norm[d0 + e];
     float mx = -INFINITY, l = 0.0f;
     const int b = d.seg_begin[r], n = d.seg_len[r];
     for (int idx = 0; idx < n; ++idx) {
       const int j = d.perm[b + idx];
       const long long mk = (long long)j * p + pi;
-      if (d.grp[mk] != gq) continue;
-      float kx[HD];
-      load(mk, 1, kx);
+      if (d.grp[mk] != gq) continue;  // same value across the 8-lane group
+      float kx[8], vx[8];
+      ld8(mk, 1, kx);
+      ld8(mk, 2, vx);
       float ks = 0.0f, dot = 0.0f;
 #pragma unroll
-      for (int dd = 0; dd < HD; ++dd) {
-        ks += kx[dd] * kx[dd];
-        dot += qn[dd] * (kx[dd] * d.k_norm[dd]);
+      for (int e = 0; e < 8; ++e) {
+        ks += kx[e] * kx[e];
+        dot += qn[e] * (kx[e] * kn[e]);
       }
-      const float s = (dot / sqrtf(ks / (float)HD + 1e-8f)) * 0.125f;
-      const float nm = fmaxf(mx, s);
-      const float corr = __expf(mx - nm), pw = __expf(s - nm);
+      ks = sum8(ks);
+      dot = sum8(dot);
+      const float sc = (dot / sqrtf(ks / (float)HD + 1e-8f)) * 0.125f;
+      const float nm = fmaxf(mx, sc);
+      const float corr = __expf(mx - nm), pw = __expf(sc - nm);
       l = l * corr + pw;
-      float vx[HD];
-      load(mk, 2, vx);
 #pragma unroll
-      for (int dd = 0; dd < HD; ++dd) o[dd] = o[dd] * corr + pw * vx[dd];
+      for (int e = 0; e < 8; ++e) o[e] = o[e] * corr + pw * vx[e];
       mx = nm;
     }
     const float inv = l > 0.0f ? 1.0f / l : 0.0f;
 #pragma unroll
-    for (int dd = 0; dd < HD; ++dd) o[dd] *= inv;
+    for (int e = 0; e < 8; ++e) o[e] *= inv;
   }
-  uint4* dst = reinterpret_cast<uint4*>(d.out + m * E + h * HD);
+  half8 hv;
 #pragma unroll
-  for (int c = 0; c < 8; ++c) {
-    half8 hv;
-#pragma unroll
-    for (int e = 0; e < 8; ++e) hv[e] = (_Float16)o[c * 8 + e];
-    dst[c] = __builtin_bit_cast(uint4, hv);
-  }
+  for (int e = 0; e < 8; ++e) hv[e] = (_Float16)o[e];
+  *reinterpret_cast<uint4*>(d.out + m * E + h * HD + d0) = __builtin_bit_cast(uint4, hv);
 }
 
 void check_hip(hipError_t e, const char* what) {
@@ -368,8 +373,8 @@ void launch_group_attention(const AttnDesc& d, hipStream_t s) {
   if (d.v <= 0 || d.p <= 0) return;
   check_common(d);
   if (!d.perm || !d.seg_begin || !d.seg_len) throw Error(T0H_ERR_INVALID_ARG, "group attention: null segment arrays");
-  const long long tasks = (long long)d.v * d.p * d.heads;
-  hipLaunchKernelGGL(k_group_attn, dim3((unsigned)((tasks + 255) / 256)), dim3(256), 0, s, d);
+  const long long lanes = (long long)d.v * d.p * d.heads * 8;
+  hipLaunchKernelGGL(k_group_attn, dim3((unsigned)((lanes + 255) / 256)), dim3(256), 0, s, d);
   check_hip(hipGetLastError(), "k_group_attn launch");
 }
 
