@@ -209,3 +209,43 @@ def test_baseline_model_forecast(t0hip, oracle, engine, rng):
     want = om.forecast(ctx, 1, 2048, 64)
     assert_close(got, want, scale=row_scale(ctx))
     assert_close(got, want)
+
+
+def test_config5_windows_small_model(t0hip, oracle, engine, rng):
+    """BASELINE config 5's window (ctx 4096: 130 patches, the long time-attention path) on a small
+    model, 2 series x 8 variates, 3 autoregressive steps of 64 against the oracle."""
+    from util import trend_season_t
+    g = t0hip.synth_model_gguf(t0hip.make_config(**SMALL), quant=8, seed=12)
+    gm = t0hip.load_model_from_gguf(engine, g)
+    om = oracle.Model(g)
+    n_series, v, t_ctx, h, steps = 2, 8, 4096, 64, 3
+    ctx = trend_season_t(rng, n_series * v, t_ctx)
+    groups = np.repeat(np.arange(n_series), v).astype(np.int64)
+    got = t0hip.forecast_grouped_ar(engine, gm, ctx, groups, t_ctx, h, steps)
+    want = om.forecast_grouped_ar(ctx, groups, t_ctx, h, steps)
+    scale = row_scale(ctx)
+    assert_close(got[:, :h], want[:, :h], scale=scale)
+    assert_close(got, want, scale=scale, tol=2e-2)
+
+
+def test_config5_full_size(t0hip, oracle, engine, rng):
+    """BASELINE config 5 at full size: 64 series x 8 variates, ctx 4096, 8 autoregressive steps of 64,
+    Q8_0 BASELINE model with weights resident across steps.  Checked by batch isolation (series 0
+    alone gives the same steps; not bit for bit, since its 16 decoder rows take the exact-f32
+    small-M GEMM while the full batch takes the f16-operand MFMA one) and, for series 0's first
+    step, against the oracle."""
+    from util import trend_season_t
+    g = t0hip.synth_model_gguf(t0hip.make_config(**BASELINE), quant=8, seed=0)
+    gm = t0hip.load_model_from_gguf(engine, g)
+    n_series, v, t_ctx, h, steps = 64, 8, 4096, 64, 8
+    ctx = trend_season_t(rng, n_series * v, t_ctx)
+    groups = np.repeat(np.arange(n_series), v).astype(np.int64)
+    full = t0hip.forecast_grouped_ar(engine, gm, ctx, groups, t_ctx, h, steps)
+    assert full.shape == (n_series * v, steps * h, 9) and np.isfinite(full).all()
+    alone = t0hip.forecast_grouped_ar(engine, gm, ctx[:v], groups[:v], t_ctx, h, steps)
+    scale = row_scale(ctx[:v])
+    assert_close(full[:v, :h], alone[:, :h], scale=scale, tol=1e-3)
+    assert_close(full[:v], alone, scale=scale, tol=2e-2)
+    om = oracle.Model(g)
+    want = om.forecast_grouped(ctx[:v], groups[:v], t_ctx, h)
+    assert_close(full[:v, :h], want, scale=scale)

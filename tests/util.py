@@ -40,3 +40,17 @@ def nan_gaps(rng, x, frac=0.1, lo=16, hi=128):
 def rel_err(got, ref):
     """max |got-ref| / max |ref| (normwise relative error)."""
     return float(np.max(np.abs(got.astype(np.float64) - ref)) / max(np.max(np.abs(ref)), 1e-30))
+
+
+def trend_season_t(rng, n_rows, t, df=3):
+    """BASELINE config 5 inputs: linear trend + two seasonal terms + Student-t(df) noise."""
+    tt = np.arange(t, dtype=np.float64)
+    slope = rng.normal(0.0, 0.01, size=(n_rows, 1))
+    level = rng.normal(0.0, 5.0, size=(n_rows, 1))
+    season = np.zeros((n_rows, t))
+    for period in (24.0, 168.0):
+        amp = rng.uniform(0.5, 3.0, size=(n_rows, 1))
+        phase = rng.uniform(0, 2 * np.pi, size=(n_rows, 1))
+        season += amp * np.sin(2 * np.pi * tt / period + phase)
+    noise = rng.standard_t(df, size=(n_rows, t)) * 0.3
+    return (level + slope * tt + season + noise).astype(np.float32)
