@@ -84,12 +84,14 @@ def gemm_sweep(torch, t0hip, iters=20):
     rng = np.random.default_rng(7)
     stream = torch.cuda.current_stream()
     out = []
-    shapes = [(768, 2304), (768, 768), (768, 2048), (2048, 768), (768, 4096)]
+    # BASELINE config 2 shapes at every M, plus one large weight (4096 x 16384) at the GEMV end,
+    # where bandwidth rather than launch latency bounds a single call
+    shapes = [(768, 2304), (768, 768), (768, 2048), (2048, 768), (768, 4096), (4096, 16384)]
     for qtype, qname, bpv in ((t0hip.Q8_0, "q8_0", 34 / 32), (t0hip.Q4_0, "q4_0", 18 / 32)):
         for K, N in shapes:
             W = (0.02 * rng.standard_normal((N, K))).astype(np.float32)
             blocks = t0hip.quantize(qtype, W)
-            for M in (1, 16, 64, 512, 8192):
+            for M in ((1, 16) if N * K > 2**24 else (1, 16, 64, 512, 8192)):
                 # rotate weight copies past the 256 MB Infinity Cache for the bandwidth-bound cases
                 n_copies = max(1, int(np.ceil(320e6 / blocks.size))) if M <= 64 else 1
                 dW = torch.from_numpy(blocks).cuda().repeat(n_copies)
@@ -281,6 +283,16 @@ def main():
     value = n_series * args.steps / elapsed
     log(f"{ms_per_step:.3f} ms/step, {value:.1f} forecasts/s")
 
+    # the same step with host buffers (t0h_forecast_grouped: context upload and result download
+    # included); reported beside `value`, never as it
+    host_steps = max(1, min(5, args.steps))
+    t0hip.forecast_grouped(engine, model, x, groups, t_ctx, horizon)
+    t0 = time.perf_counter()
+    for _ in range(host_steps):
+        t0hip.forecast_grouped(engine, model, x, groups, t_ctx, horizon)
+    host_rate = n_series * host_steps / (time.perf_counter() - t0)
+    log(f"host buffers: {host_rate:.1f} forecasts/s")
+
     # per-kernel-kind event timing inside the real forward
     model.profile(True)
     for _ in range(args.profile_steps):
@@ -326,6 +338,7 @@ def main():
         "roofline": roofline,
         "cpu_baseline": cpu,
         "forward_gemm_tflops": round(total_gemm_flops / (total_gemm_ms * 1e-3) * 1e-12, 1),
+        "host_buffers_forecasts_per_s": round(host_rate, 2),
         "kernels": kernels,
         "gemm_sweep": sweep,
     }

@@ -808,9 +808,10 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1))) voi
 }
 
 // ---------------------------------------------------------------------------
-// Small-M kernel: 16 weight rows per workgroup staged in LDS, exact f32 math.
+// Small-M kernel: 8 weight rows per workgroup staged in LDS, exact f32 math,
+// up to 4 activation rows per pass.
 // ---------------------------------------------------------------------------
-constexpr int GV_NR = 16;
+constexpr int GV_NR = 8;
 
 template <int WT>
 __device__ __forceinline__ void dequant8_lds(const uint8_t* row, int c, float (&w)[8]) {
@@ -1079,8 +1080,10 @@ template <int WT, bool A32, int EPI>
 void dispatch_gemv(const GemmDesc& d, hipStream_t s) {
   if (d.M == 1)
     run_gemv<WT, A32, EPI, 1>(d, s);
-  else
+  else if (d.M == 2)
     run_gemv<WT, A32, EPI, 2>(d, s);
+  else
+    run_gemv<WT, A32, EPI, 4>(d, s);
 }
 
 template <int WT, bool A32, int EPI>
