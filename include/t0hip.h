@@ -180,7 +180,9 @@ int t0h_gemm_q(int wtype, const void* d_w, const float* d_x, const float* d_bias
  *   3: f16 [m, n] = silu(x W_g^T + b_g) * (x W_u^T + b_u), W with 2n rows gate
  *      first (ops.rs:57-61) — the fused SwiGLU of the FFN.
  * tile: 0 = as the forward picks, 1 = 128x128, 3 = 256x256, 4 = 256x256 with
- * DMA-fed activations (K % 128 == 0, quantized weights; falls back to 1). */
+ * DMA-fed activations (K % 128 == 0, quantized weights; falls back to 1),
+ * 5 = 256x256 with the weights dequantized straight into MFMA operands
+ * (K % 64 == 0, quantized weights; falls back to 1). */
 int t0h_gemm_f16(int wtype, const void* d_w, const void* d_x, const float* d_bias, void* d_y, size_t m, size_t n,
                  size_t k, int epilogue, int tile, void* stream);
 

@@ -20,6 +20,7 @@
 #include <string>
 
 #include "kernels.h"
+#include "lanes.h"
 #include "t0hip_internal.h"
 
 namespace t0h {
@@ -47,9 +48,10 @@ size_t time_attn_lds(int p) {
 }
 
 
-// One workgroup per (variate row, head), 4 waves over the 16-query tiles.  Load phase: 8 lanes per 64-wide q/k row (16 B each), QK-RMSNorm
-// reduced over the 8-lane group, interleaved xPos RoPE on the lane's 4
-// adjacent pairs, q/k stored row-major; v rows in key pairs, transposed into
+// One workgroup per (variate row, head), 4 waves over the 16-query tiles.
+// Load phase: 8 lanes per 64-wide q/k row (16 B each), QK-RMSNorm reduced over
+// the 8-lane group, interleaved xPos RoPE on the lane's 4 adjacent pairs, q/k
+// stored row-major; v rows in key pairs, transposed into
 // LDS as (key 2i, key 2i+1) dwords.  Compute phase: per 16-query tile,
 // S^T = K Q^T and O = P V on v_mfma_f32_16x16x32_f16 with the tile's scores in
 // registers; O is staged through the tile's own Q rows and stored in 16-byte
@@ -133,9 +135,7 @@ __global__ __launch_bounds__(256) void k_time_attn(const AttnDesc d) {
       x[e] = (float)hv[e];
       ss += x[e] * x[e];
     }
-    ss += __shfl_xor(ss, 1);
-    ss += __shfl_xor(ss, 2);
-    ss += __shfl_xor(ss, 4);
+    ss = lane_sum8(ss);
     half8 o = {};
     if (i < p) {
       const float inv = 1.0f / sqrtf(ss / (float)HD + 1e-8f);
@@ -184,8 +184,7 @@ __global__ __launch_bounds__(256) void k_time_attn(const AttnDesc d) {
         }
       }
     }
-    mx = fmaxf(mx, __shfl_xor(mx, 16));
-    mx = fmaxf(mx, __shfl_xor(mx, 32));
+    mx = rows_max(mx);
     const bool uniform = mx == -INFINITY;
     float sum = 0.0f;
 #pragma unroll
@@ -200,8 +199,7 @@ __global__ __launch_bounds__(256) void k_time_attn(const AttnDesc d) {
         }
       }
     }
-    sum += __shfl_xor(sum, 16);
-    sum += __shfl_xor(sum, 32);
+    sum = rows_sum(sum);
     const float inv = 1.0f / sum;
 
     floatx4 o[4];
@@ -251,13 +249,7 @@ __global__ __launch_bounds__(256) void k_time_attn(const AttnDesc d) {
 // 64 dims; a wave covers 8 consecutive heads of a row, so every q/k/v load is
 // one contiguous 1 KB span.  Keys are the query row's group (a segment of the
 // group-sorted permutation); the norms and dot products reduce over the 8-lane
-// group with xor-shuffles; online softmax.
-__device__ __forceinline__ float sum8(float x) {
-  x += __shfl_xor(x, 1);
-  x += __shfl_xor(x, 2);
-  x += __shfl_xor(x, 4);
-  return x;
-}
+// group with DPP lane moves; online softmax.
 
 __global__ __launch_bounds__(256) void k_group_attn(const AttnDesc d) {
   const int H = d.heads, E = d.E, p = d.p, v = d.v, ld = 3 * E;
@@ -295,7 +287,7 @@ __global__ __launch_bounds__(256) void k_group_attn(const AttnDesc d) {
     float ss = 0.0f;
 #pragma unroll
     for (int e = 0; e < 8; ++e) ss += qn[e] * qn[e];
-    const float dq = sqrtf(sum8(ss) / (float)HD + 1e-8f);
+    const float dq = sqrtf(lane_sum8(ss) / (float)HD + 1e-8f);
 #pragma unroll
     for (int e = 0; e < 8; ++e) qn[e] = (qn[e] / dq) * d.q_norm[d0 + e];
     float mx = -INFINITY, l = 0.0f;
@@ -313,8 +305,8 @@ __global__ __launch_bounds__(256) void k_group_attn(const AttnDesc d) {
         ks += kx[e] * kx[e];
         dot += qn[e] * (kx[e] * kn[e]);
       }
-      ks = sum8(ks);
-      dot = sum8(dot);
+      ks = lane_sum8(ks);
+      dot = lane_sum8(dot);
       const float sc = (dot / sqrtf(ks / (float)HD + 1e-8f)) * 0.125f;
       const float nm = fmaxf(mx, sc);
       const float corr = __expf(mx - nm), pw = __expf(sc - nm);

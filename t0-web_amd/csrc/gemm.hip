@@ -32,6 +32,7 @@
 #include <string>
 
 #include "kernels.h"
+#include "lanes.h"
 #include "t0hip_internal.h"
 
 namespace t0h {
@@ -42,8 +43,9 @@ typedef _Float16 half4 __attribute__((ext_vector_type(4)));
 typedef _Float16 half2v __attribute__((ext_vector_type(2)));
 typedef float floatx4 __attribute__((ext_vector_type(4)));
 typedef float floatx16 __attribute__((ext_vector_type(16)));
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
 
-constexpr int TN = 128, TK = 64, LDK = TK + 8;
+constexpr int TK = 64, LDK = TK + 8;
 
 __host__ __device__ constexpr int block_bytes(int wt) { return wt == T0H_Q8_0 ? 34 : (wt == T0H_Q4_0 ? 18 : 0); }
 
@@ -185,6 +187,96 @@ __device__ __forceinline__ void dq_chunk(const uint32_t (&br)[16], int part, int
   }
 }
 
+// Epilogue shared by the MFMA tile kernels, staged through LDS: each wave
+// writes a 32-row slice of its results (bias, SwiGLU applied) as f32 into its
+// own LDS region, then streams the slice out in 16-byte row chunks (coalesced
+// f32/f16 stores, vector residual read-modify-write).  acc[i][j] is the wave's
+// 32x32 tile (rows row_base + 32 i, tile column group j); in each tile lane l
+// holds column l%32, rows (e/4)*8 + (l/32)*4 + e%4.  SwiGLU: groups j < TJ/2
+// are gate columns and j + TJ/2 the up columns of the same hidden units, so the
+// wave writes TJ*16 output columns from cbase; otherwise TJ*32.  `smemf` needs
+// (waves) * 32 * (W + 4) floats and must be free (callers end their main loop
+// with a barrier).
+template <int EPI, int TI, int TJ>
+__device__ __forceinline__ void store_tile(const GemmDesc& d, floatx16 (&acc)[TI][TJ], float* smemf, int wave,
+                                           int lane, int row_base, int cbase) {
+  constexpr bool SWI = EPI == EPI_SWIGLU_F16;
+  constexpr int W = SWI ? TJ * 16 : TJ * 32;  // output columns per wave
+  constexpr int SLD = W + 4;                  // staging row stride (floats)
+  constexpr int NJ = SWI ? TJ / 2 : TJ;       // staged 32-column groups per wave
+  const int M = d.M, N = d.N;
+  float* stage = smemf + wave * 32 * SLD;
+  const int lc = lane & 31, lr = (lane >> 5) * 4;
+  float b0[NJ], b1[NJ];
+#pragma unroll
+  for (int j = 0; j < NJ; ++j) {
+    const int col = cbase + j * 32 + lc;
+    const bool ok = d.bias && col < N;
+    b0[j] = ok ? d.bias[col] : 0.0f;
+    b1[j] = (SWI && ok) ? d.bias[N + col] : 0.0f;
+  }
+  const bool vec_ok = (d.ldy & 3) == 0 && (N & 3) == 0;
+#pragma unroll
+  for (int i = 0; i < TI; ++i) {
+#pragma unroll
+    for (int e = 0; e < 16; ++e) {
+      const int r = (e >> 2) * 8 + lr + (e & 3);
+#pragma unroll
+      for (int j = 0; j < NJ; ++j)
+        stage[r * SLD + j * 32 + lc] =
+            SWI ? silu(acc[i][j][e] + b0[j]) * (acc[i][j + TJ / 2][e] + b1[j]) : acc[i][j][e] + b0[j];
+    }
+    __syncthreads();
+    const int row0 = row_base + i * 32;
+#pragma unroll
+    for (int t = 0; t < W / 8; ++t) {
+      const int idx = t * 64 + lane;
+      const int r = idx / (W / 4), c = (idx % (W / 4)) * 4;
+      const int row = row0 + r, col = cbase + c;
+      if (row >= M || col >= N) continue;
+      float4 v = *reinterpret_cast<const float4*>(stage + r * SLD + c);
+      const size_t o = (size_t)row * d.ldy + col;
+      if (vec_ok) {
+        if (EPI == EPI_STORE_F32 && d.row_add) {
+          const float4 t4 = *reinterpret_cast<const float4*>(d.row_add + (size_t)d.row_add_idx[row] * N + col);
+          v.x += t4.x; v.y += t4.y; v.z += t4.z; v.w += t4.w;
+        }
+        if ((EPI == EPI_STORE_F32 || EPI == EPI_STORE_F16) && d.relu) {
+          v.x = fmaxf(v.x, 0.0f); v.y = fmaxf(v.y, 0.0f); v.z = fmaxf(v.z, 0.0f); v.w = fmaxf(v.w, 0.0f);
+        }
+        if (EPI == EPI_RESID_F32) {
+          float4* y = reinterpret_cast<float4*>(static_cast<float*>(d.y) + o);
+          const float4 old = *y;
+          *y = make_float4(old.x + v.x, old.y + v.y, old.z + v.z, old.w + v.w);
+        } else if (EPI == EPI_STORE_F32) {
+          *reinterpret_cast<float4*>(static_cast<float*>(d.y) + o) = v;
+        } else {
+          half4 h = {(_Float16)v.x, (_Float16)v.y, (_Float16)v.z, (_Float16)v.w};
+          *reinterpret_cast<half4*>(static_cast<_Float16*>(d.y) + o) = h;
+        }
+      } else {
+        const float vv[4] = {v.x, v.y, v.z, v.w};
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+          if (col + q >= N) break;
+          float x = vv[q];
+          if (EPI == EPI_STORE_F32 && d.row_add) x += d.row_add[(size_t)d.row_add_idx[row] * N + col + q];
+          if ((EPI == EPI_STORE_F32 || EPI == EPI_STORE_F16) && d.relu) x = fmaxf(x, 0.0f);
+          if (EPI == EPI_RESID_F32) {
+            float* y = static_cast<float*>(d.y) + o + q;
+            *y = *y + x;
+          } else if (EPI == EPI_STORE_F32) {
+            static_cast<float*>(d.y)[o + q] = x;
+          } else {
+            static_cast<_Float16*>(d.y)[o + q] = (_Float16)x;
+          }
+        }
+      }
+    }
+    if (i + 1 < TI) __syncthreads();
+  }
+}
+
 template <int WT, bool A32, int EPI, bool K64, int TI, int TJ>
 __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(Tile<TI, TJ>::WPE, Tile<TI, TJ>::WPE)))
 void k_gemm(const GemmDesc d) {
@@ -214,11 +306,26 @@ void k_gemm(const GemmDesc d) {
   // each 64-wide K step (32 activations; one 32-value weight block).  Rows
   // past M read row M-1 and weight rows past N read row 0: their outputs are
   // never stored, and the loads stay branch-free.
+  // f16 activations with K % 64 == 0 (ROWA) load by row instead: lanes
+  // 8j..8j+7 of a wave read the 128 bytes of one row, so each 16-byte load
+  // instruction covers 8 whole cache lines (the half-row split above touches
+  // 32 lines per instruction, and the L1 tag lookups bound the main loop).
+  // Thread t moves 16-byte chunk t%8 of rows t/8 + 32 q + 128 r.
+  constexpr bool ROWA = !A32 && K64;
   const int lrow = tid >> 1, lh = tid & 1;
-  const char* abase[RA];
+  const int arow = tid >> 3, achunk = tid & 7;
+  const char* abase[RA][ROWA ? 4 : 1];
 #pragma unroll
-  for (int r = 0; r < RA; ++r)
-    abase[r] = static_cast<const char*>(d.a) + (size_t)min(m0 + lrow + 128 * r, M - 1) * d.lda * (A32 ? 4 : 2);
+  for (int r = 0; r < RA; ++r) {
+    if constexpr (ROWA) {
+#pragma unroll
+      for (int q = 0; q < 4; ++q)
+        abase[r][q] = static_cast<const char*>(d.a) + (size_t)min(m0 + arow + 32 * q + 128 * r, M - 1) * d.lda * 2 +
+                      achunk * 16;
+    } else {
+      abase[r][0] = static_cast<const char*>(d.a) + (size_t)min(m0 + lrow + 128 * r, M - 1) * d.lda * (A32 ? 4 : 2);
+    }
+  }
   const size_t rowb = WT == T0H_F16 ? (size_t)K * 2 : (size_t)(K / 32) * block_bytes(WT);
   const uint8_t* wbase[RB];
 #pragma unroll
@@ -252,8 +359,17 @@ void k_gemm(const GemmDesc d) {
     const int k0c = (K64 || k0 < K) ? k0 : k0 - 32;
 #pragma unroll
     for (int r = 0; r < RA; ++r) {
-      if (A32) {
-        const float4* src = reinterpret_cast<const float4*>(reinterpret_cast<const float*>(abase[r]) + k0c);
+      if constexpr (ROWA) {
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+          const uint4 v = *reinterpret_cast<const uint4*>(abase[r][q] + kt * (TK * 2));
+          st.a[r][4 * q + 0] = v.x;
+          st.a[r][4 * q + 1] = v.y;
+          st.a[r][4 * q + 2] = v.z;
+          st.a[r][4 * q + 3] = v.w;
+        }
+      } else if (A32) {
+        const float4* src = reinterpret_cast<const float4*>(reinterpret_cast<const float*>(abase[r][0]) + k0c);
 #pragma unroll
         for (int i = 0; i < 8; ++i) {
           const float4 v = src[i];
@@ -263,7 +379,7 @@ void k_gemm(const GemmDesc d) {
           st.a[r][4 * i + 3] = __builtin_bit_cast(uint32_t, v.w);
         }
       } else {
-        const uint4* src = reinterpret_cast<const uint4*>(reinterpret_cast<const _Float16*>(abase[r]) + k0c);
+        const uint4* src = reinterpret_cast<const uint4*>(reinterpret_cast<const _Float16*>(abase[r][0]) + k0c);
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
           const uint4 v = src[i];
@@ -311,13 +427,17 @@ void k_gemm(const GemmDesc d) {
       }
     }
   };
+  // LDS offset (elements) of this thread's 16-byte A chunk q of row group r
+  auto a_lds = [&](int r, int q) {
+    return ROWA ? (arow + 32 * q + 128 * r) * LDK + achunk * 8 : (lrow + 128 * r) * LDK + lh * 32 + 8 * q;
+  };
   auto write = [&](const uint32_t (&ao)[RA][16], const uint32_t (&wo)[RB][16], int buf) {
 #pragma unroll
-    for (int r = 0; r < RA; ++r) {
-      uint4* dst = reinterpret_cast<uint4*>(As + (size_t)buf * BM * LDK + (lrow + 128 * r) * LDK + lh * 32);
+    for (int r = 0; r < RA; ++r)
 #pragma unroll
-      for (int i = 0; i < 4; ++i) dst[i] = make_uint4(ao[r][4 * i], ao[r][4 * i + 1], ao[r][4 * i + 2], ao[r][4 * i + 3]);
-    }
+      for (int i = 0; i < 4; ++i)
+        *reinterpret_cast<uint4*>(As + (size_t)buf * BM * LDK + a_lds(r, i)) =
+            make_uint4(ao[r][4 * i], ao[r][4 * i + 1], ao[r][4 * i + 2], ao[r][4 * i + 3]);
 #pragma unroll
     for (int r = 0; r < RB; ++r) {
       uint4* dst = reinterpret_cast<uint4*>(Bs + (size_t)buf * BN * LDK + (lrow + 128 * r) * LDK + lh * 32);
@@ -391,7 +511,7 @@ void k_gemm(const GemmDesc d) {
 #pragma unroll
       for (int r = 0; r < RB; ++r) dd[r] = dq_scale<WT, true>(st.b[r], lh);
       uint32_t wo[RB][16];
-      _Float16* An = As + (size_t)(buf ^ 1) * BM * LDK + lrow * LDK + lh * 32;
+      _Float16* An = As + (size_t)(buf ^ 1) * BM * LDK;
       _Float16* Bn = Bs + (size_t)(buf ^ 1) * BN * LDK + lrow * LDK + lh * 32;
       const _Float16* At = As + (size_t)buf * BM * LDK + (wm * (BM / 2) + (lane & 31)) * LDK + (lane >> 5) * 8;
       const _Float16* Bt = Bs + (size_t)buf * BN * LDK + (lane & 31) * LDK + (lane >> 5) * 8;
@@ -428,7 +548,7 @@ void k_gemm(const GemmDesc d) {
                 if (w * NMS / NW == mi) {
                   if (w < 4 * RA) {
                     const int r = w / 4, q = w % 4;
-                    *reinterpret_cast<uint4*>(An + 128 * r * LDK + 8 * q) =
+                    *reinterpret_cast<uint4*>(An + a_lds(r, q)) =
                         make_uint4(st.a[r][4 * q], st.a[r][4 * q + 1], st.a[r][4 * q + 2], st.a[r][4 * q + 3]);
                   } else {
                     const int r = (w - 4 * RA) / 4, q = (w - 4 * RA) % 4;
@@ -457,11 +577,18 @@ void k_gemm(const GemmDesc d) {
     load_global(s1, min(1, last));
     store_lds(s0, 0, 0);
     __syncthreads();
-    for (int kt = 0; kt < KT; kt += 2) {
+    // Pairs of steps with one loop exit (an exit between the two steps makes
+    // the compiler copy the accumulators every step); an odd last step runs
+    // after the loop.
+    int kt = 0;
+    for (; kt + 1 < KT; kt += 2) {
       step2(0, s0, min(kt + 2, last), s1);
       __syncthreads();
-      if (kt + 1 >= KT) break;
       step2(1, s1, min(kt + 3, last), s0);
+      __syncthreads();
+    }
+    if (kt < KT) {
+      step2(0, s0, last, s1);
       __syncthreads();
     }
   } else {
@@ -479,85 +606,9 @@ void k_gemm(const GemmDesc d) {
     }
   }
 
-  // Epilogue, staged through LDS (free after the main loop's last barrier):
-  // each wave writes a 32-row slice of its results (bias, SwiGLU applied) as
-  // f32 into its own LDS region, then streams the slice out in 16-byte row
-  // chunks (coalesced f32/f16 stores, vector residual read-modify-write).
-  // In each 32x32 MFMA tile lane l holds column l%32, rows (e/4)*8 + (l/32)*4 + e%4.
-  constexpr int W = SWI ? TJ * 16 : TJ * 32;  // output columns per wave
-  constexpr int SLD = W + 4;                  // staging row stride (floats)
-  constexpr int NJ = SWI ? TJ / 2 : TJ;       // staged 32-column groups per wave
-  float* stage = reinterpret_cast<float*>(smem) + wave * 32 * SLD;
-  const int cbase = SWI ? tn * HB + wn * (HB / 2) : tn * BN + wn * (BN / 2);  // first output column
-  const int lc = lane & 31, lr = (lane >> 5) * 4;
-  float b0[NJ], b1[NJ];
-#pragma unroll
-  for (int j = 0; j < NJ; ++j) {
-    const int col = cbase + j * 32 + lc;
-    const bool ok = d.bias && col < N;
-    b0[j] = ok ? d.bias[col] : 0.0f;
-    b1[j] = (SWI && ok) ? d.bias[N + col] : 0.0f;
-  }
-  const bool vec_ok = (d.ldy & 3) == 0 && (N & 3) == 0;
-#pragma unroll
-  for (int i = 0; i < TI; ++i) {
-#pragma unroll
-    for (int e = 0; e < 16; ++e) {
-      const int r = (e >> 2) * 8 + lr + (e & 3);
-#pragma unroll
-      for (int j = 0; j < NJ; ++j)
-        stage[r * SLD + j * 32 + lc] =
-            SWI ? silu(acc[i][j][e] + b0[j]) * (acc[i][j + TJ / 2][e] + b1[j]) : acc[i][j][e] + b0[j];
-    }
-    __syncthreads();
-    const int row0 = m0 + wm * (BM / 2) + i * 32;
-#pragma unroll
-    for (int t = 0; t < W / 8; ++t) {
-      const int idx = t * 64 + lane;
-      const int r = idx / (W / 4), c = (idx % (W / 4)) * 4;
-      const int row = row0 + r, col = cbase + c;
-      if (row >= M || col >= N) continue;
-      float4 v = *reinterpret_cast<const float4*>(stage + r * SLD + c);
-      const size_t o = (size_t)row * d.ldy + col;
-      if (vec_ok) {
-        if (EPI == EPI_STORE_F32 && d.row_add) {
-          const float4 t4 = *reinterpret_cast<const float4*>(d.row_add + (size_t)d.row_add_idx[row] * N + col);
-          v.x += t4.x; v.y += t4.y; v.z += t4.z; v.w += t4.w;
-        }
-        if ((EPI == EPI_STORE_F32 || EPI == EPI_STORE_F16) && d.relu) {
-          v.x = fmaxf(v.x, 0.0f); v.y = fmaxf(v.y, 0.0f); v.z = fmaxf(v.z, 0.0f); v.w = fmaxf(v.w, 0.0f);
-        }
-        if (EPI == EPI_RESID_F32) {
-          float4* y = reinterpret_cast<float4*>(static_cast<float*>(d.y) + o);
-          const float4 old = *y;
-          *y = make_float4(old.x + v.x, old.y + v.y, old.z + v.z, old.w + v.w);
-        } else if (EPI == EPI_STORE_F32) {
-          *reinterpret_cast<float4*>(static_cast<float*>(d.y) + o) = v;
-        } else {
-          half4 h = {(_Float16)v.x, (_Float16)v.y, (_Float16)v.z, (_Float16)v.w};
-          *reinterpret_cast<half4*>(static_cast<_Float16*>(d.y) + o) = h;
-        }
-      } else {
-        const float vv[4] = {v.x, v.y, v.z, v.w};
-#pragma unroll
-        for (int q = 0; q < 4; ++q) {
-          if (col + q >= N) break;
-          float x = vv[q];
-          if (EPI == EPI_STORE_F32 && d.row_add) x += d.row_add[(size_t)d.row_add_idx[row] * N + col + q];
-          if ((EPI == EPI_STORE_F32 || EPI == EPI_STORE_F16) && d.relu) x = fmaxf(x, 0.0f);
-          if (EPI == EPI_RESID_F32) {
-            float* y = static_cast<float*>(d.y) + o + q;
-            *y = *y + x;
-          } else if (EPI == EPI_STORE_F32) {
-            static_cast<float*>(d.y)[o + q] = x;
-          } else {
-            static_cast<_Float16*>(d.y)[o + q] = (_Float16)x;
-          }
-        }
-      }
-    }
-    if (i + 1 < TI) __syncthreads();
-  }
+  // LDS is free after the main loop's last barrier: stage the epilogue in it.
+  store_tile<EPI, TI, TJ>(d, acc, reinterpret_cast<float*>(smem), wave, lane, m0 + wm * (BM / 2),
+                          SWI ? tn * HB + wn * (HB / 2) : tn * BN + wn * (BN / 2));
 }
 
 // ---------------------------------------------------------------------------
@@ -751,60 +802,233 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1))) voi
   __builtin_amdgcn_s_waitcnt(0 | (7 << 4) | (15 << 8));
   __syncthreads();
 
-  // Epilogue (as k_gemm): per-wave 32-row slices staged in LDS as f32.
-  constexpr int W = SWI ? TJ * 16 : TJ * 32;
-  constexpr int SLD = W + 4;
-  constexpr int NJ = SWI ? TJ / 2 : TJ;
-  float* stage = reinterpret_cast<float*>(smem) + wave * 32 * SLD;
-  const int cbase = SWI ? tn * HB + wn * (HB / 2) : tn * DM_BN + wn * (DM_BN / 2);
-  const int lc = lane & 31, lr = (lane >> 5) * 4;
-  float b0[NJ], b1[NJ];
+  store_tile<EPI, TI, TJ>(d, acc, reinterpret_cast<float*>(smem), wave, lane, m0 + wm * (DM_BM / 2),
+                          SWI ? tn * HB + wn * (HB / 2) : tn * DM_BN + wn * (DM_BN / 2));
+}
+
+// ---------------------------------------------------------------------------
+// Register-B tile kernel: 256x256x64 tiles for K % 64 == 0, f16 activations
+// and Q8_0/Q4_0 weights.  NWV = 4 waves of 128x128 (4x4 tiles of
+// v_mfma_f32_32x32x16_f16, one wave per SIMD) or 8 waves of 128x64 (4x2
+// tiles, two waves per SIMD); accumulators in AGPRs.
+//  * Weights never pass through LDS: each lane loads the raw 18/34-byte block
+//    of its own weight row and dequantizes it straight into MFMA B fragments.
+//    Inside a 64-wide K step the k order is permuted so that lane half h owns
+//    block h: MFMA slice c takes k = 32h + 8c .. 32h + 8c + 7 of the step,
+//    i.e. the Q4_0 nibbles of qs bytes 8(c%2) .. +7 (low for c < 2, high for
+//    c >= 2) or Q8_0 qs bytes 8c .. +7.  The activation fragments follow the
+//    same order, so every product of the step is still summed once.
+//  * Activations: row-coalesced 16-byte loads (8 lanes per 128-byte row) two
+//    steps ahead into three LDS buffers; the first fragments of step kt+1 are
+//    read before step kt's closing barrier, so no step starts on an LDS wait.
+//  * The work between MFMAs is spread evenly: one dequantization sub-step
+//    (about four VALU instructions) after each MFMA, the next slice's A
+//    fragment reads after the first four, and the step's global loads one per
+//    MFMA through the first slice.  Measured on MI355X, a wave's VALU work
+//    beyond ~5 instructions per MFMA adds to the MFMA time instead of
+//    overlapping it, and bursts of loads right after a barrier stall issue.
+// ---------------------------------------------------------------------------
+constexpr int BF_BM = 256, BF_BN = 256;
+constexpr int BF_ABUF = BF_BM * LDK;    // halves per activation buffer
+constexpr int BF_LDS = 3 * BF_ABUF * 2;  // 110,592 bytes (the epilogue stage needs <= 69,632)
+
+template <int WT, int EPI, int NWV>
+__global__ __launch_bounds__(64 * NWV) __attribute__((amdgpu_waves_per_eu(NWV / 4, NWV / 4)))
+void k_gemm_bf(const GemmDesc d) {
+  constexpr int WNW = NWV / 2;                  // waves along N (2 along M)
+  constexpr int TI = 4, TJ = BF_BN / WNW / 32;  // 32x32 tiles per wave
+  constexpr int ACH = 2048 / (64 * NWV);        // 16-byte activation chunks per thread and step
+  constexpr int AQS = BF_BM / ACH;              // row stride between a thread's chunks
+  constexpr int NMS = TI * TJ;                  // MFMAs per slice
+  constexpr bool SWI = EPI == EPI_SWIGLU_F16;
+  constexpr int HB = SWI ? BF_BN / 2 : BF_BN;    // output columns per tile
+  constexpr int NWD = WT == T0H_Q8_0 ? 9 : 5;    // raw dwords a lane needs per column and step
+  constexpr int SWD = WT == T0H_Q8_0 ? 17 : 9;   // dwords of one row's two blocks (one step)
+  static_assert(NMS == 4 * TJ && NMS >= TI + ACH && NMS >= ACH + TJ, "slice work placement");
+  extern __shared__ __align__(16) _Float16 smem[];
+
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int wm = wave / WNW, wn = wave % WNW, h = lane >> 5, lc = lane & 31;
+  const int M = d.M, N = d.N, K = d.K;
+  const int tiles_n = (N + HB - 1) / HB;
+  const int total = gridDim.x, bid = blockIdx.x;
+  const int per = total / 8;
+  const int logical = bid < per * 8 ? (bid % 8) * per + bid / 8 : bid;
+  const int tm = logical / tiles_n, tn = logical % tiles_n;
+  const int m0 = tm * BF_BM;
+  const int KT = K / TK, last = KT - 1;
+
+  // Activation loads: thread t moves 16-byte chunk t%8 of rows t/8 + AQS q;
+  // byte offsets from the tile's first row (32-bit: a tile spans < 2 GiB).
+  // Rows past M read row M-1 (never stored).
+  const int arow = tid >> 3, achunk = tid & 7;
+  const char* const a_tile = static_cast<const char*>(d.a) + (size_t)m0 * d.lda * 2;
+  int aoff[ACH];
 #pragma unroll
-  for (int j = 0; j < NJ; ++j) {
-    const int col = cbase + j * 32 + lc;
-    const bool ok = d.bias && col < N;
-    b0[j] = ok ? d.bias[col] : 0.0f;
-    b1[j] = (SWI && ok) ? d.bias[N + col] : 0.0f;
+  for (int q = 0; q < ACH; ++q) aoff[q] = (min(m0 + arow + AQS * q, M - 1) - m0) * d.lda * 2 + achunk * 16;
+
+  // Weight rows of the lane's column tiles (SwiGLU: the first half of the
+  // tiles gate rows, the second half the up rows of the same hidden units);
+  // rows past N read row 0.  The lane reads dwords (h ? NWD-1 : 0) .. +NWD of
+  // each step's 2-block span: block h and, for h = 0, the two bytes of block
+  // 1 that end the last dword.  Dword offsets: the weights are < 16 GiB.
+  const int rowd = (K / 32) * block_bytes(WT) / 4;
+  const uint32_t* const wbase = static_cast<const uint32_t*>(d.w);
+  int woff[TJ];
+#pragma unroll
+  for (int j = 0; j < TJ; ++j) {
+    int wrow;
+    bool ok;
+    if (SWI) {
+      const int g = tn * HB + wn * (HB / WNW) + (j % (TJ / 2)) * 32 + lc;
+      ok = g < N;
+      wrow = j < TJ / 2 ? g : N + g;
+    } else {
+      wrow = tn * BF_BN + wn * (BF_BN / WNW) + j * 32 + lc;
+      ok = wrow < N;
+    }
+    woff[j] = (ok ? wrow : 0) * rowd + h * (NWD - 1);
   }
+  // block h starts 2 bytes into the lane's first dword (h = 0) or at its
+  // second dword (h = 1), after the scale in the first dword's high half
+  const uint32_t qsel = h ? 0x07060504u : 0x05040302u;
+  const uint32_t dsel = h ? 0x03020302u : 0x01000100u;
+
+  u32x4 ar[ACH];
+  auto load_a1 = [&](int kt, int q) {
+    ar[q] = *reinterpret_cast<const u32x4*>(a_tile + kt * (TK * 2) + aoff[q]);
+  };
+  auto a_dst = [&](int buf, int q) {
+    return reinterpret_cast<u32x4*>(smem + buf * BF_ABUF + (arow + AQS * q) * LDK + achunk * 8);
+  };
+  auto load_b1 = [&](uint32_t (&r)[NWD], int kt, int j) {
+    const uint32_t* src = wbase + (uint32_t)(woff[j] + kt * SWD);  // NWD contiguous dwords
 #pragma unroll
-  for (int i = 0; i < TI; ++i) {
+    for (int i = 0; i < NWD; ++i) r[i] = src[i];
+  };
+  const _Float16* afr_base = smem + (wm * 128 + lc) * LDK + h * 32;
+  auto read_a = [&](int buf, int c, int i) {
+    return *reinterpret_cast<const half8*>(afr_base + buf * BF_ABUF + i * 32 * LDK + c * 8);
+  };
+
+  // B fragment of slice c from a lane's raw dwords r, in four sub-steps of
+  // about four VALU instructions each (one fragment in flight at a time).
+  uint32_t ts[4];
+  half2v tdd;
+  auto dq = [&](const uint32_t (&r)[NWD], int c, int sub, half8& out) {
+    if (sub == 0) {
+      const int i = WT == T0H_Q8_0 ? 2 * c : 2 * (c & 1);
+      uint32_t qa = perm(r[i + 1], r[i], qsel), qb = perm(r[i + 2], r[i + 1], qsel);
+      if (WT == T0H_Q4_0) {
+        if (c >= 2) {
+          qa >>= 4;
+          qb >>= 4;
+        }
+        qa &= 0x0f0f0f0fu;
+        qb &= 0x0f0f0f0fu;
+      } else {
+        qa ^= 0x80808080u;
+        qb ^= 0x80808080u;
+      }
+      ts[0] = qa;
+      ts[1] = qb;
+      tdd = __builtin_bit_cast(half2v, perm(r[0], r[0], dsel));
+    } else if (sub == 1) {
+      ts[2] = perm(0x64646464u, ts[1], 0x04010400u);
+      ts[3] = perm(0x64646464u, ts[1], 0x04030402u);
+      ts[1] = perm(0x64646464u, ts[0], 0x04030402u);
+      ts[0] = perm(0x64646464u, ts[0], 0x04010400u);
+    } else if (sub == 2) {
+      const _Float16 o = (_Float16)(WT == T0H_Q8_0 ? 1152.0f : 1032.0f);
+      const half2v off = {o, o};
 #pragma unroll
-    for (int e = 0; e < 16; ++e) {
-      const int r = (e >> 2) * 8 + lr + (e & 3);
+      for (int e = 0; e < 4; ++e) ts[e] = __builtin_bit_cast(uint32_t, __builtin_bit_cast(half2v, ts[e]) - off);
+    } else {
+      uint32_t o[4];
 #pragma unroll
-      for (int j = 0; j < NJ; ++j)
-        stage[r * SLD + j * 32 + lc] =
-            SWI ? silu(acc[i][j][e] + b0[j]) * (acc[i][j + TJ / 2][e] + b1[j]) : acc[i][j][e] + b0[j];
+      for (int e = 0; e < 4; ++e) o[e] = __builtin_bit_cast(uint32_t, __builtin_bit_cast(half2v, ts[e]) * tdd);
+      out = __builtin_bit_cast(half8, make_uint4(o[0], o[1], o[2], o[3]));
+    }
+#pragma unroll
+    for (int e = 0; e < 4; ++e) asm volatile("" : "+v"(ts[e]));
+  };
+
+  floatx16 acc[TI][TJ];
+#pragma unroll
+  for (int i = 0; i < TI; ++i)
+#pragma unroll
+    for (int j = 0; j < TJ; ++j)
+#pragma unroll
+      for (int e = 0; e < 16; ++e) acc[i][j][e] = 0.0f;
+
+  uint32_t wr0[TJ][NWD], wr1[TJ][NWD];
+  half8 af[2][TI], bf[2][TJ];
+
+  // Prologue: activations of steps 0 and 1 into buffers 0 and 1, weights of
+  // step 0, and the slice-0 fragments of step 0.
+#pragma unroll
+  for (int q = 0; q < ACH; ++q) load_a1(0, q);
+#pragma unroll
+  for (int j = 0; j < TJ; ++j) load_b1(wr0[j], 0, j);
+#pragma unroll
+  for (int q = 0; q < ACH; ++q) *a_dst(0, q) = ar[q];
+#pragma unroll
+  for (int q = 0; q < ACH; ++q) load_a1(min(1, last), q);
+#pragma unroll
+  for (int q = 0; q < ACH; ++q) *a_dst(1, q) = ar[q];
+  __syncthreads();
+#pragma unroll
+  for (int i = 0; i < TI; ++i) af[0][i] = read_a(0, 0, i);
+#pragma unroll
+  for (int j = 0; j < TJ; ++j)
+#pragma unroll
+    for (int sub = 0; sub < 4; ++sub) dq(wr0[j], 0, sub, bf[0][j]);
+
+  // One step: four slices of NMS MFMAs, each MFMA followed by a share of the
+  // next slice's operands (A fragment i after MFMA i, B fragment j's
+  // sub-step s after MFMA 4j+s) and, in the first slice, by one of the step's
+  // global loads (A(kt+2) chunks, then W(kt+1) columns).  The last slice
+  // prepares slice 0 of step kt+1 (its A buffer is complete since the previous
+  // barrier) and writes A(kt+2) to the third buffer.
+  int abuf = 0;
+  auto step = [&](int kt, uint32_t (&cur)[TJ][NWD], uint32_t (&nxt)[TJ][NWD]) {
+    const int b1 = abuf == 2 ? 0 : abuf + 1, b2 = b1 == 2 ? 0 : b1 + 1;
+    const int ka = min(kt + 2, last), kb = min(kt + 1, last);
+#pragma unroll
+    for (int c = 0; c < 4; ++c) {
+      const int p = c & 1, n = p ^ 1;
+#pragma unroll
+      for (int i = 0; i < TI; ++i)
+#pragma unroll
+        for (int j = 0; j < TJ; ++j) {
+          const int mi = i * TJ + j;
+          acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(af[p][i], bf[p][j], acc[i][j], 0, 0, 0);
+          if (c == 0 && mi < ACH) load_a1(ka, mi);
+          if (c == 0 && mi >= ACH && mi < ACH + TJ) load_b1(nxt[mi - ACH], kb, mi - ACH);
+          if (mi < TI) af[n][mi] = read_a(c < 3 ? abuf : b1, c < 3 ? c + 1 : 0, mi);
+          if (c < 3)
+            dq(cur[mi >> 2], c + 1, mi & 3, bf[n][mi >> 2]);
+          else
+            dq(nxt[mi >> 2], 0, mi & 3, bf[n][mi >> 2]);
+          if (c == 3 && mi >= TI && mi < TI + ACH) *a_dst(b2, mi - TI) = ar[mi - TI];
+          __builtin_amdgcn_sched_barrier(0);
+        }
     }
     __syncthreads();
-    const int row0 = m0 + wm * (DM_BM / 2) + i * 32;
-#pragma unroll
-    for (int t = 0; t < W / 8; ++t) {
-      const int idx = t * 64 + lane;
-      const int r = idx / (W / 4), c = (idx % (W / 4)) * 4;
-      const int row = row0 + r, col = cbase + c;
-      if (row >= M || col >= N) continue;
-      float4 v = *reinterpret_cast<const float4*>(stage + r * SLD + c);
-      const size_t o = (size_t)row * d.ldy + col;
-      if (EPI == EPI_RESID_F32) {
-        float4* y = reinterpret_cast<float4*>(static_cast<float*>(d.y) + o);
-        const float4 old = *y;
-        *y = make_float4(old.x + v.x, old.y + v.y, old.z + v.z, old.w + v.w);
-      } else if (EPI == EPI_STORE_F32) {
-        if (d.row_add) {
-          const float4 t4 = *reinterpret_cast<const float4*>(d.row_add + (size_t)d.row_add_idx[row] * N + col);
-          v.x += t4.x; v.y += t4.y; v.z += t4.z; v.w += t4.w;
-        }
-        if (d.relu) { v.x = fmaxf(v.x, 0.0f); v.y = fmaxf(v.y, 0.0f); v.z = fmaxf(v.z, 0.0f); v.w = fmaxf(v.w, 0.0f); }
-        *reinterpret_cast<float4*>(static_cast<float*>(d.y) + o) = v;
-      } else {
-        if (EPI == EPI_STORE_F16 && d.relu) { v.x = fmaxf(v.x, 0.0f); v.y = fmaxf(v.y, 0.0f); v.z = fmaxf(v.z, 0.0f); v.w = fmaxf(v.w, 0.0f); }
-        half4 h = {(_Float16)v.x, (_Float16)v.y, (_Float16)v.z, (_Float16)v.w};
-        *reinterpret_cast<half4*>(static_cast<_Float16*>(d.y) + o) = h;
-      }
-    }
-    if (i + 1 < TI) __syncthreads();
+    abuf = b1;
+  };
+
+  // Pairs of steps with one loop exit (the weight stages alternate); an odd
+  // last step runs after the loop.
+  int kt = 0;
+  for (; kt + 1 < KT; kt += 2) {
+    step(kt, wr0, wr1);
+    step(kt + 1, wr1, wr0);
   }
+  if (kt < KT) step(kt, wr0, wr1);
+
+  store_tile<EPI, TI, TJ>(d, acc, reinterpret_cast<float*>(smem), wave, lane, m0 + wm * (BF_BM / 2),
+                          SWI ? tn * HB + wn * (HB / WNW) : tn * BF_BN + wn * (BF_BN / WNW));
 }
 
 // ---------------------------------------------------------------------------
@@ -1046,6 +1270,22 @@ void run_gemm_dma(const GemmDesc& d, hipStream_t s) {
   check_hip(hipGetLastError(), "k_gemm_dma launch");
 }
 
+template <int WT, int EPI, int NWV>
+void run_gemm_bf(const GemmDesc& d, hipStream_t s) {
+  const int hb = EPI == EPI_SWIGLU_F16 ? BF_BN / 2 : BF_BN;
+  const int tiles_n = (d.N + hb - 1) / hb;
+  const int tiles_m = (d.M + BF_BM - 1) / BF_BM;
+  static bool attr_set = false;
+  if (!attr_set) {
+    check_hip(hipFuncSetAttribute(reinterpret_cast<const void*>(&k_gemm_bf<WT, EPI, NWV>),
+                                  hipFuncAttributeMaxDynamicSharedMemorySize, BF_LDS),
+              "hipFuncSetAttribute(k_gemm_bf)");
+    attr_set = true;
+  }
+  hipLaunchKernelGGL((k_gemm_bf<WT, EPI, NWV>), dim3(tiles_m * tiles_n), dim3(64 * NWV), BF_LDS, s, d);
+  check_hip(hipGetLastError(), "k_gemm_bf launch");
+}
+
 template <int WT, bool A32, int EPI, bool K64>
 void run_gemm_tiled(const GemmDesc& d, int tile, hipStream_t s) {
   // By shape (tile 0): 128x128 everywhere.  Measured in the config-4 forward,
@@ -1054,6 +1294,8 @@ void run_gemm_tiled(const GemmDesc& d, int tile, hipStream_t s) {
   if (tile == 0) tile = 1;
   if constexpr (!A32 && K64 && WT != T0H_F16) {
     if (tile == 4 && dma_ok(d)) return run_gemm_dma<WT, EPI>(d, s);
+    if (tile == 5) return run_gemm_bf<WT, EPI, 8>(d, s);
+    if (tile == 6) return run_gemm_bf<WT, EPI, 4>(d, s);
   }
   if constexpr (!A32 && K64) {
     if (tile == 3 || tile == 4) return run_gemm<WT, A32, EPI, K64, 4, 4>(d, s);

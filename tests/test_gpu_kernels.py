@@ -144,16 +144,9 @@ def test_gemm_linearity_and_zero_weights(torch_cuda, t0hip, oracle, rng):
 FWD_SHAPES = {0: (768, 768), 1: (768, 2304), 2: (2048, 768), 3: (768, 2048)}
 
 
-@pytest.mark.parametrize("qtype", [8, 2])
-@pytest.mark.parametrize("tile", [1, 3, 4])
-@pytest.mark.parametrize("epi", [0, 1, 2, 3])
-def test_forward_gemm_paths(torch_cuda, t0hip, oracle, rng, qtype, tile, epi):
-    """linear() (model.rs:406-504) as the forward runs it: f16 x, f32 accumulation,
-    epilogues bias / f16 store / residual add / SwiGLU (ops.rs:49-62); 1e-2 relative
-    on a 512-row sample of M = 4192 rows."""
-    torch = torch_cuda
-    k, n = FWD_SHAPES[epi]
-    m = 4192
+def check_forward_gemm(torch, t0hip, oracle, rng, qtype, tile, epi, m, k, n, sample=True):
+    """Run t0h_gemm_f16 on random data and compare with float64 over the
+    oracle's dequantized weights: 1e-2 relative."""
     wrows = 2 * n if epi == 3 else n
     W = (0.02 * rng.standard_normal((wrows, k))).astype(np.float32)
     b = (0.02 * rng.standard_normal(wrows)).astype(np.float32)
@@ -168,7 +161,10 @@ def test_forward_gemm_paths(torch_cuda, t0hip, oracle, rng, qtype, tile, epi):
                        torch.cuda.current_stream().cuda_stream)
     torch.cuda.synchronize()
     got = d_y.float().cpu().numpy()
-    rows = np.sort(np.concatenate([rng.choice(m - 200, 312, replace=False), np.arange(m - 200, m)]))
+    if sample:
+        rows = np.sort(np.concatenate([rng.choice(m - 200, 312, replace=False), np.arange(m - 200, m)]))
+    else:
+        rows = np.arange(m)
     h = x16[rows].astype(np.float64) @ deq.T + b
     if epi == 3:
         g, u = h[:, :n], h[:, n:]
@@ -178,4 +174,28 @@ def test_forward_gemm_paths(torch_cuda, t0hip, oracle, rng, qtype, tile, epi):
     else:
         want = h
     e = rel_err(got[rows], want)
-    assert e < 1e-2, e
+    assert e < 1e-2, (tile, epi, m, k, n, e)
+
+
+@pytest.mark.parametrize("qtype", [8, 2])
+@pytest.mark.parametrize("tile", [1, 3, 4, 5])
+@pytest.mark.parametrize("epi", [0, 1, 2, 3])
+def test_forward_gemm_paths(torch_cuda, t0hip, oracle, rng, qtype, tile, epi):
+    """linear() (model.rs:406-504) as the forward runs it: f16 x, f32 accumulation,
+    epilogues bias / f16 store / residual add / SwiGLU (ops.rs:49-62); 1e-2 relative
+    on a 512-row sample of M = 4192 rows (ragged against every tile height)."""
+    k, n = FWD_SHAPES[epi]
+    check_forward_gemm(torch_cuda, t0hip, oracle, rng, qtype, tile, epi, 4192, k, n)
+
+
+@pytest.mark.parametrize("qtype", [8, 2])
+@pytest.mark.parametrize("epi", [0, 1, 2, 3])
+@pytest.mark.parametrize("m,k,n", [(300, 192, 328), (257, 64, 330), (40, 128, 72)])
+def test_register_b_gemm_edges(torch_cuda, t0hip, oracle, rng, qtype, epi, m, k, n):
+    """The 256x256 register-operand kernel (tile 5) on partial tiles: M and N
+    ragged (weight rows past N clamp to row 0), an odd number of 64-wide K steps
+    (the step after the paired loop), one step, and N % 4 != 0 (scalar stores;
+    SwiGLU needs N % 8 == 0 and takes n rounded down to 8)."""
+    if epi == 3:
+        n -= n % 8
+    check_forward_gemm(torch_cuda, t0hip, oracle, rng, qtype, 5, epi, m, k, n, sample=False)
