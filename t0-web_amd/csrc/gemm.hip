@@ -832,19 +832,22 @@ constexpr int BF_BM = 256, BF_BN = 256;
 constexpr int BF_ABUF = BF_BM * LDK;    // halves per activation buffer
 constexpr int BF_LDS = 3 * BF_ABUF * 2;  // 110,592 bytes (the epilogue stage needs <= 69,632)
 
-template <int WT, int EPI, int NWV>
+template <int WT, int EPI, int NWV, int WMW>
 __global__ __launch_bounds__(64 * NWV) __attribute__((amdgpu_waves_per_eu(NWV / 4, NWV / 4)))
 void k_gemm_bf(const GemmDesc d) {
-  constexpr int WNW = NWV / 2;                  // waves along N (2 along M)
-  constexpr int TI = 4, TJ = BF_BN / WNW / 32;  // 32x32 tiles per wave
+  constexpr int WNW = NWV / WMW;                // waves along N (WMW along M)
+  constexpr int TI = BF_BM / 32 / WMW;          // 32x32 tiles per wave: TI rows ...
+  constexpr int TJ = BF_BN / WNW / 32;          // ... by TJ columns
   constexpr int ACH = 2048 / (64 * NWV);        // 16-byte activation chunks per thread and step
   constexpr int AQS = BF_BM / ACH;              // row stride between a thread's chunks
   constexpr int NMS = TI * TJ;                  // MFMAs per slice
   constexpr bool SWI = EPI == EPI_SWIGLU_F16;
+  static_assert(!SWI || TJ % 2 == 0, "SwiGLU pairs gate and up tiles inside a wave");
   constexpr int HB = SWI ? BF_BN / 2 : BF_BN;    // output columns per tile
   constexpr int NWD = WT == T0H_Q8_0 ? 9 : 5;    // raw dwords a lane needs per column and step
   constexpr int SWD = WT == T0H_Q8_0 ? 17 : 9;   // dwords of one row's two blocks (one step)
-  static_assert(NMS == 4 * TJ && NMS >= TI + ACH && NMS >= ACH + TJ, "slice work placement");
+  static_assert(TJ == 1 ? (NMS == 8 && ACH <= 4) : (NMS == 4 * TJ && NMS >= TI + ACH && NMS >= ACH + TJ),
+                "slice work placement");
   extern __shared__ __align__(16) _Float16 smem[];
 
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
@@ -906,7 +909,7 @@ void k_gemm_bf(const GemmDesc d) {
 #pragma unroll
     for (int i = 0; i < NWD; ++i) r[i] = src[i];
   };
-  const _Float16* afr_base = smem + (wm * 128 + lc) * LDK + h * 32;
+  const _Float16* afr_base = smem + (wm * (BF_BM / WMW) + lc) * LDK + h * 32;
   auto read_a = [&](int buf, int c, int i) {
     return *reinterpret_cast<const half8*>(afr_base + buf * BF_ABUF + i * 32 * LDK + c * 8);
   };
@@ -966,19 +969,32 @@ void k_gemm_bf(const GemmDesc d) {
 
   // Prologue: activations of steps 0 and 1 into buffers 0 and 1, weights of
   // step 0, and the slice-0 fragments of step 0.
+  {
+    u32x4 ar1[ACH];
 #pragma unroll
-  for (int q = 0; q < ACH; ++q) load_a1(0, q);
+    for (int q = 0; q < ACH; ++q) load_a1(0, q);
 #pragma unroll
-  for (int j = 0; j < TJ; ++j) load_b1(wr0[j], 0, j);
+    for (int q = 0; q < ACH; ++q) ar1[q] = *reinterpret_cast<const u32x4*>(a_tile + min(1, last) * (TK * 2) + aoff[q]);
 #pragma unroll
-  for (int q = 0; q < ACH; ++q) *a_dst(0, q) = ar[q];
+    for (int j = 0; j < TJ; ++j) load_b1(wr0[j], 0, j);
 #pragma unroll
-  for (int q = 0; q < ACH; ++q) load_a1(min(1, last), q);
+    for (int q = 0; q < ACH; ++q) *a_dst(0, q) = ar[q];
 #pragma unroll
-  for (int q = 0; q < ACH; ++q) *a_dst(1, q) = ar[q];
+    for (int q = 0; q < ACH; ++q) *a_dst(1, q) = ar1[q];
+  }
   __syncthreads();
+  // TJ == 1: each A fragment feeds one MFMA, so fragments stream through a
+  // ring read RD MFMAs ahead (RING divides the 4*TI MFMAs of a step, so slots
+  // line up across steps).
+  constexpr int RING = 8, RD = 4;
+  half8 ring[RING];
+  if constexpr (TJ == 1) {
 #pragma unroll
-  for (int i = 0; i < TI; ++i) af[0][i] = read_a(0, 0, i);
+    for (int m = 0; m < RD; ++m) ring[m] = read_a(0, m / TI, m % TI);
+  } else {
+#pragma unroll
+    for (int i = 0; i < TI; ++i) af[0][i] = read_a(0, 0, i);
+  }
 #pragma unroll
   for (int j = 0; j < TJ; ++j)
 #pragma unroll
@@ -994,6 +1010,36 @@ void k_gemm_bf(const GemmDesc d) {
   auto step = [&](int kt, uint32_t (&cur)[TJ][NWD], uint32_t (&nxt)[TJ][NWD]) {
     const int b1 = abuf == 2 ? 0 : abuf + 1, b2 = b1 == 2 ? 0 : b1 + 1;
     const int ka = min(kt + 2, last), kb = min(kt + 1, last);
+    if constexpr (TJ == 1) {
+      // Slice c, MFMA i (m = c*TI + i): the ring read of fragment m + RD (in
+      // step kt+1 once past the step: its buffer is complete), B sub-steps
+      // after every other MFMA, the A(kt+2) chunk loads and the W(kt+1) load
+      // in the first slice, the A(kt+2) stores early in the last.
+      constexpr int NMI = 4 * TI;
+#pragma unroll
+      for (int c = 0; c < 4; ++c) {
+        const int p = c & 1, n = p ^ 1;
+#pragma unroll
+        for (int i = 0; i < TI; ++i) {
+          const int m = c * TI + i, mr = m + RD;
+          acc[i][0] = __builtin_amdgcn_mfma_f32_32x32x16_f16(ring[m % RING], bf[p][0], acc[i][0], 0, 0, 0);
+          ring[mr % RING] = mr < NMI ? read_a(abuf, mr / TI, mr % TI) : read_a(b1, 0, mr - NMI);
+          if (c == 0 && i < ACH) load_a1(ka, i);
+          if (c == 0 && i == ACH) load_b1(nxt[0], kb, 0);
+          if ((i & 1) == 0) {
+            if (c < 3)
+              dq(cur[0], c + 1, i >> 1, bf[n][0]);
+            else
+              dq(nxt[0], 0, i >> 1, bf[n][0]);
+          }
+          if (c == 3 && i < ACH) *a_dst(b2, i) = ar[i];
+          __builtin_amdgcn_sched_barrier(0);
+        }
+      }
+      __syncthreads();
+      abuf = b1;
+      return;
+    }
 #pragma unroll
     for (int c = 0; c < 4; ++c) {
       const int p = c & 1, n = p ^ 1;
@@ -1027,7 +1073,7 @@ void k_gemm_bf(const GemmDesc d) {
   }
   if (kt < KT) step(kt, wr0, wr1);
 
-  store_tile<EPI, TI, TJ>(d, acc, reinterpret_cast<float*>(smem), wave, lane, m0 + wm * (BF_BM / 2),
+  store_tile<EPI, TI, TJ>(d, acc, reinterpret_cast<float*>(smem), wave, lane, m0 + wm * (BF_BM / WMW),
                           SWI ? tn * HB + wn * (HB / WNW) : tn * BF_BN + wn * (BF_BN / WNW));
 }
 
@@ -1270,32 +1316,44 @@ void run_gemm_dma(const GemmDesc& d, hipStream_t s) {
   check_hip(hipGetLastError(), "k_gemm_dma launch");
 }
 
-template <int WT, int EPI, int NWV>
+template <int WT, int EPI, int NWV, int WMW>
 void run_gemm_bf(const GemmDesc& d, hipStream_t s) {
   const int hb = EPI == EPI_SWIGLU_F16 ? BF_BN / 2 : BF_BN;
   const int tiles_n = (d.N + hb - 1) / hb;
   const int tiles_m = (d.M + BF_BM - 1) / BF_BM;
   static bool attr_set = false;
   if (!attr_set) {
-    check_hip(hipFuncSetAttribute(reinterpret_cast<const void*>(&k_gemm_bf<WT, EPI, NWV>),
+    check_hip(hipFuncSetAttribute(reinterpret_cast<const void*>(&k_gemm_bf<WT, EPI, NWV, WMW>),
                                   hipFuncAttributeMaxDynamicSharedMemorySize, BF_LDS),
               "hipFuncSetAttribute(k_gemm_bf)");
     attr_set = true;
   }
-  hipLaunchKernelGGL((k_gemm_bf<WT, EPI, NWV>), dim3(tiles_m * tiles_n), dim3(64 * NWV), BF_LDS, s, d);
+  hipLaunchKernelGGL((k_gemm_bf<WT, EPI, NWV, WMW>), dim3(tiles_m * tiles_n), dim3(64 * NWV), BF_LDS, s, d);
   check_hip(hipGetLastError(), "k_gemm_bf launch");
 }
 
 template <int WT, bool A32, int EPI, bool K64>
 void run_gemm_tiled(const GemmDesc& d, int tile, hipStream_t s) {
-  // By shape (tile 0): 128x128 everywhere.  Measured in the config-4 forward,
-  // 128x128 at two workgroups per CU beat the 256x256 tiles (one workgroup per
-  // CU, DMA-fed or not) and 256x128 at every layer shape.
-  if (tile == 0) tile = 1;
+  // By shape (tile 0).  Measured at the config-4 layer shapes (M = 50,688,
+  // Q4_0): the register-operand 256x256 kernel takes the wide outputs (QKV
+  // N = 2304: 239 us vs 290 us for 128x128; SwiGLU N = 2048: 393 us vs
+  // 430 us); at N = 768 its 3 column tiles leave the last of ~2.3 rounds of
+  // workgroups mostly idle, and 128x128 at two workgroups per CU is as fast
+  // (wO) or faster (w2: 253 us vs 265 us).  The DMA and plain 256x256 tiles
+  // lose at every shape.
+  if (tile == 0) {
+    tile = 1;
+    if constexpr (!A32 && K64 && WT != T0H_F16)
+      if (d.M >= 1024 && (EPI == EPI_SWIGLU_F16 || d.N >= 1536)) tile = 5;
+  }
   if constexpr (!A32 && K64 && WT != T0H_F16) {
     if (tile == 4 && dma_ok(d)) return run_gemm_dma<WT, EPI>(d, s);
-    if (tile == 5) return run_gemm_bf<WT, EPI, 8>(d, s);
-    if (tile == 6) return run_gemm_bf<WT, EPI, 4>(d, s);
+    if (tile == 5) {
+      if constexpr (EPI == EPI_SWIGLU_F16) return run_gemm_bf<WT, EPI, 8, 2>(d, s);
+      else return run_gemm_bf<WT, EPI, 8, 1>(d, s);
+    }
+    if (tile == 6) return run_gemm_bf<WT, EPI, 8, 2>(d, s);
+    if (tile == 7) return run_gemm_bf<WT, EPI, 4, 2>(d, s);
   }
   if constexpr (!A32 && K64) {
     if (tile == 3 || tile == 4) return run_gemm<WT, A32, EPI, K64, 4, 4>(d, s);
