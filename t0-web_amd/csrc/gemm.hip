@@ -201,32 +201,50 @@ template <int EPI, int TI, int TJ>
 __device__ __forceinline__ void store_tile(const GemmDesc& d, floatx16 (&acc)[TI][TJ], float* smemf, int wave,
                                            int lane, int row_base, int cbase) {
   constexpr bool SWI = EPI == EPI_SWIGLU_F16;
-  constexpr int W = SWI ? TJ * 16 : TJ * 32;  // output columns per wave
-  constexpr int SLD = W + 4;                  // staging row stride (floats)
-  constexpr int NJ = SWI ? TJ / 2 : TJ;       // staged 32-column groups per wave
+  // SwiGLU with one column group (PAIR): lanes l%32 < 16 hold the gate and
+  // lanes l%32 >= 16 the up column of the same 16 hidden units.
+  constexpr bool PAIR = SWI && TJ == 1;
+  constexpr int W = PAIR ? 16 : (SWI ? TJ * 16 : TJ * 32);  // output columns per wave
+  constexpr int SLD = W + 4;                                 // staging row stride (floats)
+  constexpr int NJ = SWI && !PAIR ? TJ / 2 : TJ;             // staged column groups per wave
   const int M = d.M, N = d.N;
   float* stage = smemf + wave * 32 * SLD;
-  const int lc = lane & 31, lr = (lane >> 5) * 4;
+  const int lc = lane & 31, lr = (lane >> 5) * 4, uc = PAIR ? (lc & 15) : lc;
   float b0[NJ], b1[NJ];
 #pragma unroll
   for (int j = 0; j < NJ; ++j) {
-    const int col = cbase + j * 32 + lc;
+    const int col = cbase + j * 32 + uc;
     const bool ok = d.bias && col < N;
     b0[j] = ok ? d.bias[col] : 0.0f;
     b1[j] = (SWI && ok) ? d.bias[N + col] : 0.0f;
   }
   const bool vec_ok = (d.ldy & 3) == 0 && (N & 3) == 0;
+  // Each wave stages into and reads back from its own region, and a wave's
+  // LDS operations complete in order: no barrier is needed.
 #pragma unroll
   for (int i = 0; i < TI; ++i) {
+    if constexpr (PAIR) {
+      // Results e and e+1 swap across the 16-lane rows: rows 0/2 (gate lanes)
+      // end with (gate, up) of result e, rows 1/3 (up lanes) with those of
+      // result e+1, so every lane forms one distinct output of unit l%16.
 #pragma unroll
-    for (int e = 0; e < 16; ++e) {
-      const int r = (e >> 2) * 8 + lr + (e & 3);
+      for (int e = 0; e < 16; e += 2) {
+        const auto gu = __builtin_amdgcn_permlane16_swap(__float_as_uint(acc[i][0][e]),
+                                                         __float_as_uint(acc[i][0][e + 1]), false, false);
+        const float v = silu(__uint_as_float(gu[0]) + b0[0]) * (__uint_as_float(gu[1]) + b1[0]);
+        const int ee = e + (lc >> 4);
+        stage[((ee >> 2) * 8 + lr + (ee & 3)) * SLD + uc] = v;
+      }
+    } else {
 #pragma unroll
-      for (int j = 0; j < NJ; ++j)
-        stage[r * SLD + j * 32 + lc] =
-            SWI ? silu(acc[i][j][e] + b0[j]) * (acc[i][j + TJ / 2][e] + b1[j]) : acc[i][j][e] + b0[j];
+      for (int e = 0; e < 16; ++e) {
+        const int r = (e >> 2) * 8 + lr + (e & 3);
+#pragma unroll
+        for (int j = 0; j < NJ; ++j)
+          stage[r * SLD + j * 32 + lc] =
+              SWI ? silu(acc[i][j][e] + b0[j]) * (acc[i][j + TJ / 2][e] + b1[j]) : acc[i][j][e] + b0[j];
+      }
     }
-    __syncthreads();
     const int row0 = row_base + i * 32;
 #pragma unroll
     for (int t = 0; t < W / 8; ++t) {
@@ -273,7 +291,6 @@ __device__ __forceinline__ void store_tile(const GemmDesc& d, floatx16 (&acc)[TI
         }
       }
     }
-    if (i + 1 < TI) __syncthreads();
   }
 }
 
@@ -807,115 +824,105 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1))) voi
 }
 
 // ---------------------------------------------------------------------------
-// Register-B tile kernel: 256x256x64 tiles for K % 64 == 0, f16 activations
-// and Q8_0/Q4_0 weights.  NWV = 4 waves of 128x128 (4x4 tiles of
-// v_mfma_f32_32x32x16_f16, one wave per SIMD) or 8 waves of 128x64 (4x2
-// tiles, two waves per SIMD); accumulators in AGPRs.
+// Register-operand tile kernel: 256x256x64 tiles for K % 64 == 0, f16
+// activations and Q8_0/Q4_0 weights.  Eight waves side by side along N, each
+// all 256 rows x 32 weight columns as 8 tiles of v_mfma_f32_32x32x16_f16
+// (128 accumulators, two waves per SIMD, one workgroup per CU).
 //  * Weights never pass through LDS: each lane loads the raw 18/34-byte block
-//    of its own weight row and dequantizes it straight into MFMA B fragments.
-//    Inside a 64-wide K step the k order is permuted so that lane half h owns
-//    block h: MFMA slice c takes k = 32h + 8c .. 32h + 8c + 7 of the step,
-//    i.e. the Q4_0 nibbles of qs bytes 8(c%2) .. +7 (low for c < 2, high for
-//    c >= 2) or Q8_0 qs bytes 8c .. +7.  The activation fragments follow the
-//    same order, so every product of the step is still summed once.
+//    of its own weight row and dequantizes it straight into the MFMA B
+//    fragment, so every weight column is dequantized once per tile (about two
+//    VALU instructions per MFMA).  Inside a 64-wide K step the k order is
+//    permuted so that lane half h owns block h: MFMA slice c takes
+//    k = 32h + 8c .. 32h + 8c + 7 of the step, i.e. the Q4_0 nibbles of qs
+//    bytes 8(c%2) .. +7 (low for c < 2, high for c >= 2) or Q8_0 qs bytes
+//    8c .. +7.  The activation fragments follow the same order, so every
+//    product of the step is still summed once.  SwiGLU: lanes l%32 < 16 take
+//    the gate rows and the others the up rows of the same 16 hidden units.
 //  * Activations: row-coalesced 16-byte loads (8 lanes per 128-byte row) two
-//    steps ahead into three LDS buffers; the first fragments of step kt+1 are
-//    read before step kt's closing barrier, so no step starts on an LDS wait.
-//  * The work between MFMAs is spread evenly: one dequantization sub-step
-//    (about four VALU instructions) after each MFMA, the next slice's A
-//    fragment reads after the first four, and the step's global loads one per
-//    MFMA through the first slice.  Measured on MI355X, a wave's VALU work
-//    beyond ~5 instructions per MFMA adds to the MFMA time instead of
+//    steps ahead into three LDS buffers.  Each A fragment feeds
+//    one MFMA; fragments stream through a ring read RD MFMAs ahead, across
+//    the step's barrier into the next step (whose buffer is complete).
+//  * Between MFMAs: one ring read, a dequantization sub-step (about four VALU
+//    instructions) after every other MFMA, and in the first slice the step's
+//    global loads, one per MFMA.  Measured on MI355X, a wave's VALU work
+//    beyond a few instructions per MFMA adds to the MFMA time instead of
 //    overlapping it, and bursts of loads right after a barrier stall issue.
 // ---------------------------------------------------------------------------
-constexpr int BF_BM = 256, BF_BN = 256;
+constexpr int BF_BM = 256, BF_BN = 256, BF_NW = 8;
 constexpr int BF_ABUF = BF_BM * LDK;    // halves per activation buffer
-constexpr int BF_LDS = 3 * BF_ABUF * 2;  // 110,592 bytes (the epilogue stage needs <= 69,632)
+constexpr int BF_LDS = 3 * BF_ABUF * 2;  // 110,592 bytes
 
-template <int WT, int EPI, int NWV, int WMW>
-__global__ __launch_bounds__(64 * NWV) __attribute__((amdgpu_waves_per_eu(NWV / 4, NWV / 4)))
-void k_gemm_bf(const GemmDesc d) {
-  constexpr int WNW = NWV / WMW;                // waves along N (WMW along M)
-  constexpr int TI = BF_BM / 32 / WMW;          // 32x32 tiles per wave: TI rows ...
-  constexpr int TJ = BF_BN / WNW / 32;          // ... by TJ columns
-  constexpr int ACH = 2048 / (64 * NWV);        // 16-byte activation chunks per thread and step
-  constexpr int AQS = BF_BM / ACH;              // row stride between a thread's chunks
-  constexpr int NMS = TI * TJ;                  // MFMAs per slice
+template <int WT, int EPI>
+__global__ __launch_bounds__(64 * BF_NW) __attribute__((amdgpu_waves_per_eu(2, 2))) void k_gemm_bf(const GemmDesc d) {
+  constexpr int TI = BF_BM / 32, TJ = 1;      // 32x32 tiles per wave
+  constexpr int ACH = 2048 / (64 * BF_NW);    // 16-byte activation chunks per thread and step (4)
+  constexpr int AQS = BF_BM / ACH;            // row stride between a thread's chunks
+  constexpr int NMI = 4 * TI;                 // MFMAs per step
+  constexpr int RING = 8, RD = 6;             // A fragment ring; RING divides NMI
   constexpr bool SWI = EPI == EPI_SWIGLU_F16;
-  static_assert(!SWI || TJ % 2 == 0, "SwiGLU pairs gate and up tiles inside a wave");
   constexpr int HB = SWI ? BF_BN / 2 : BF_BN;    // output columns per tile
-  constexpr int NWD = WT == T0H_Q8_0 ? 9 : 5;    // raw dwords a lane needs per column and step
+  constexpr int NWD = WT == T0H_Q8_0 ? 9 : 5;    // raw dwords a lane needs per step
   constexpr int SWD = WT == T0H_Q8_0 ? 17 : 9;   // dwords of one row's two blocks (one step)
-  static_assert(TJ == 1 ? (NMS == 8 && ACH <= 4) : (NMS == 4 * TJ && NMS >= TI + ACH && NMS >= ACH + TJ),
-                "slice work placement");
+  static_assert(NMI % RING == 0 && RD < RING && ACH < TI, "step work placement");
+  static_assert(BF_NW * 32 * ((SWI ? 16 : 32) + 4) * 4 <= BF_LDS, "epilogue stage fits the LDS");
   extern __shared__ __align__(16) _Float16 smem[];
 
-  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-  const int wm = wave / WNW, wn = wave % WNW, h = lane >> 5, lc = lane & 31;
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6, h = lane >> 5, lc = lane & 31;
   const int M = d.M, N = d.N, K = d.K;
   const int tiles_n = (N + HB - 1) / HB;
-  const int total = gridDim.x, bid = blockIdx.x;
-  const int per = total / 8;
-  const int logical = bid < per * 8 ? (bid % 8) * per + bid / 8 : bid;
-  const int tm = logical / tiles_n, tn = logical % tiles_n;
-  const int m0 = tm * BF_BM;
   const int KT = K / TK, last = KT - 1;
+  // XCD-aware remap (blocks are dispatched round-robin over 8 XCDs): each
+  // XCD gets a contiguous range of logical tiles, N fastest, so concurrent
+  // tiles share activation rows in that XCD's L2.
+  const int total = gridDim.x, bid = blockIdx.x, per = total / 8;
+  const int t = bid < per * 8 ? (bid % 8) * per + bid / 8 : bid;
+  const int tn = t % tiles_n, m0 = (t / tiles_n) * BF_BM;
 
-  // Activation loads: thread t moves 16-byte chunk t%8 of rows t/8 + AQS q;
-  // byte offsets from the tile's first row (32-bit: a tile spans < 2 GiB).
-  // Rows past M read row M-1 (never stored).
+  // Activation chunk t%8 of rows t/8 + AQS q (rows past M read row M-1,
+  // never stored) as byte offsets from the tile's first row; the lane's weight
+  // row (rows past N read row 0) as a dword offset, plus the dwords
+  // (h ? NWD-1 : 0) of each step's 2-block span.
   const int arow = tid >> 3, achunk = tid & 7;
   const char* const a_tile = static_cast<const char*>(d.a) + (size_t)m0 * d.lda * 2;
   int aoff[ACH];
 #pragma unroll
   for (int q = 0; q < ACH; ++q) aoff[q] = (min(m0 + arow + AQS * q, M - 1) - m0) * d.lda * 2 + achunk * 16;
-
-  // Weight rows of the lane's column tiles (SwiGLU: the first half of the
-  // tiles gate rows, the second half the up rows of the same hidden units);
-  // rows past N read row 0.  The lane reads dwords (h ? NWD-1 : 0) .. +NWD of
-  // each step's 2-block span: block h and, for h = 0, the two bytes of block
-  // 1 that end the last dword.  Dword offsets: the weights are < 16 GiB.
-  const int rowd = (K / 32) * block_bytes(WT) / 4;
-  const uint32_t* const wbase = static_cast<const uint32_t*>(d.w);
-  int woff[TJ];
-#pragma unroll
-  for (int j = 0; j < TJ; ++j) {
+  int woff;
+  {
     int wrow;
     bool ok;
     if (SWI) {
-      const int g = tn * HB + wn * (HB / WNW) + (j % (TJ / 2)) * 32 + lc;
+      const int g = tn * HB + wave * 16 + (lc & 15);
       ok = g < N;
-      wrow = j < TJ / 2 ? g : N + g;
+      wrow = lc < 16 ? g : N + g;
     } else {
-      wrow = tn * BF_BN + wn * (BF_BN / WNW) + j * 32 + lc;
+      wrow = tn * BF_BN + wave * 32 + lc;
       ok = wrow < N;
     }
-    woff[j] = (ok ? wrow : 0) * rowd + h * (NWD - 1);
+    woff = (ok ? wrow : 0) * ((K / 32) * block_bytes(WT) / 4) + h * (NWD - 1);
   }
+  const uint32_t* const wbase = static_cast<const uint32_t*>(d.w);
   // block h starts 2 bytes into the lane's first dword (h = 0) or at its
   // second dword (h = 1), after the scale in the first dword's high half
   const uint32_t qsel = h ? 0x07060504u : 0x05040302u;
   const uint32_t dsel = h ? 0x03020302u : 0x01000100u;
 
-  u32x4 ar[ACH];
-  auto load_a1 = [&](int kt, int q) {
-    ar[q] = *reinterpret_cast<const u32x4*>(a_tile + kt * (TK * 2) + aoff[q]);
-  };
+  auto load_a = [&](u32x4& r, int kt, int q) { r = *reinterpret_cast<const u32x4*>(a_tile + kt * (TK * 2) + aoff[q]); };
   auto a_dst = [&](int buf, int q) {
     return reinterpret_cast<u32x4*>(smem + buf * BF_ABUF + (arow + AQS * q) * LDK + achunk * 8);
   };
-  auto load_b1 = [&](uint32_t (&r)[NWD], int kt, int j) {
-    const uint32_t* src = wbase + (uint32_t)(woff[j] + kt * SWD);  // NWD contiguous dwords
+  auto load_b = [&](uint32_t (&r)[NWD], int kt) {
+    const uint32_t* src = wbase + (uint32_t)(woff + kt * SWD);  // NWD contiguous dwords
 #pragma unroll
     for (int i = 0; i < NWD; ++i) r[i] = src[i];
   };
-  const _Float16* afr_base = smem + (wm * (BF_BM / WMW) + lc) * LDK + h * 32;
+  const _Float16* afr_base = smem + lc * LDK + h * 32;
   auto read_a = [&](int buf, int c, int i) {
     return *reinterpret_cast<const half8*>(afr_base + buf * BF_ABUF + i * 32 * LDK + c * 8);
   };
 
-  // B fragment of slice c from a lane's raw dwords r, in four sub-steps of
-  // about four VALU instructions each (one fragment in flight at a time).
+  // B fragment of slice c from the lane's raw dwords r, in four sub-steps of
+  // about four VALU instructions each.
   uint32_t ts[4];
   half2v tdd;
   auto dq = [&](const uint32_t (&r)[NWD], int c, int sub, half8& out) {
@@ -960,109 +967,62 @@ void k_gemm_bf(const GemmDesc d) {
 #pragma unroll
   for (int i = 0; i < TI; ++i)
 #pragma unroll
-    for (int j = 0; j < TJ; ++j)
+    for (int e = 0; e < 16; ++e) acc[i][0][e] = 0.0f;
+  uint32_t wr0[NWD], wr1[NWD];
+  half8 ring[RING], bf[2];
+  u32x4 ar[ACH];
+
+  int abuf = 0;
+  // One step: slice c, MFMA i (m = c*TI + i): the ring read of fragment
+  // m + RD (in step kt+1 once past the step), B sub-steps after every other
+  // MFMA, the A(kt+2) chunk loads and the W(kt+1) load in the first slice,
+  // the A(kt+2) stores in the last.
+  auto step = [&](int kt, uint32_t (&cur)[NWD], uint32_t (&nxt)[NWD]) {
+    const int b1 = abuf == 2 ? 0 : abuf + 1, b2 = b1 == 2 ? 0 : b1 + 1;
+    const int kb = min(kt + 1, last), ka = min(kt + 2, last);
 #pragma unroll
-      for (int e = 0; e < 16; ++e) acc[i][j][e] = 0.0f;
+    for (int c = 0; c < 4; ++c) {
+      const int p = c & 1, n = p ^ 1;
+#pragma unroll
+      for (int i = 0; i < TI; ++i) {
+        const int m = c * TI + i, mr = m + RD;
+        acc[i][0] = __builtin_amdgcn_mfma_f32_32x32x16_f16(ring[m % RING], bf[p], acc[i][0], 0, 0, 0);
+        ring[mr % RING] = mr < NMI ? read_a(abuf, mr / TI, mr % TI) : read_a(b1, 0, mr - NMI);
+        if (c == 0 && i < ACH) load_a(ar[i], ka, i);
+        if (c == 0 && i == ACH) load_b(nxt, kb);
+        if ((i & 1) == 0) {
+          if (c < 3)
+            dq(cur, c + 1, i >> 1, bf[n]);
+          else
+            dq(nxt, 0, i >> 1, bf[n]);
+        }
+        if (c == 3 && i < ACH) *a_dst(b2, i) = ar[i];
+        __builtin_amdgcn_sched_barrier(0);
+      }
+    }
+    __syncthreads();
+    abuf = b1;
+  };
 
-  uint32_t wr0[TJ][NWD], wr1[TJ][NWD];
-  half8 af[2][TI], bf[2][TJ];
-
-  // Prologue: activations of steps 0 and 1 into buffers 0 and 1, weights of
-  // step 0, and the slice-0 fragments of step 0.
+  // Prologue: A(0), A(1) into buffers 0 and 1, W(0), the first ring
+  // fragments and the slice-0 B fragment.
   {
     u32x4 ar1[ACH];
 #pragma unroll
-    for (int q = 0; q < ACH; ++q) load_a1(0, q);
+    for (int q = 0; q < ACH; ++q) load_a(ar[q], 0, q);
 #pragma unroll
-    for (int q = 0; q < ACH; ++q) ar1[q] = *reinterpret_cast<const u32x4*>(a_tile + min(1, last) * (TK * 2) + aoff[q]);
-#pragma unroll
-    for (int j = 0; j < TJ; ++j) load_b1(wr0[j], 0, j);
+    for (int q = 0; q < ACH; ++q) load_a(ar1[q], min(1, last), q);
+    load_b(wr0, 0);
 #pragma unroll
     for (int q = 0; q < ACH; ++q) *a_dst(0, q) = ar[q];
 #pragma unroll
     for (int q = 0; q < ACH; ++q) *a_dst(1, q) = ar1[q];
   }
   __syncthreads();
-  // TJ == 1: each A fragment feeds one MFMA, so fragments stream through a
-  // ring read RD MFMAs ahead (RING divides the 4*TI MFMAs of a step, so slots
-  // line up across steps).
-  constexpr int RING = 8, RD = 4;
-  half8 ring[RING];
-  if constexpr (TJ == 1) {
 #pragma unroll
-    for (int m = 0; m < RD; ++m) ring[m] = read_a(0, m / TI, m % TI);
-  } else {
+  for (int m = 0; m < RD; ++m) ring[m] = read_a(0, m / TI, m % TI);
 #pragma unroll
-    for (int i = 0; i < TI; ++i) af[0][i] = read_a(0, 0, i);
-  }
-#pragma unroll
-  for (int j = 0; j < TJ; ++j)
-#pragma unroll
-    for (int sub = 0; sub < 4; ++sub) dq(wr0[j], 0, sub, bf[0][j]);
-
-  // One step: four slices of NMS MFMAs, each MFMA followed by a share of the
-  // next slice's operands (A fragment i after MFMA i, B fragment j's
-  // sub-step s after MFMA 4j+s) and, in the first slice, by one of the step's
-  // global loads (A(kt+2) chunks, then W(kt+1) columns).  The last slice
-  // prepares slice 0 of step kt+1 (its A buffer is complete since the previous
-  // barrier) and writes A(kt+2) to the third buffer.
-  int abuf = 0;
-  auto step = [&](int kt, uint32_t (&cur)[TJ][NWD], uint32_t (&nxt)[TJ][NWD]) {
-    const int b1 = abuf == 2 ? 0 : abuf + 1, b2 = b1 == 2 ? 0 : b1 + 1;
-    const int ka = min(kt + 2, last), kb = min(kt + 1, last);
-    if constexpr (TJ == 1) {
-      // Slice c, MFMA i (m = c*TI + i): the ring read of fragment m + RD (in
-      // step kt+1 once past the step: its buffer is complete), B sub-steps
-      // after every other MFMA, the A(kt+2) chunk loads and the W(kt+1) load
-      // in the first slice, the A(kt+2) stores early in the last.
-      constexpr int NMI = 4 * TI;
-#pragma unroll
-      for (int c = 0; c < 4; ++c) {
-        const int p = c & 1, n = p ^ 1;
-#pragma unroll
-        for (int i = 0; i < TI; ++i) {
-          const int m = c * TI + i, mr = m + RD;
-          acc[i][0] = __builtin_amdgcn_mfma_f32_32x32x16_f16(ring[m % RING], bf[p][0], acc[i][0], 0, 0, 0);
-          ring[mr % RING] = mr < NMI ? read_a(abuf, mr / TI, mr % TI) : read_a(b1, 0, mr - NMI);
-          if (c == 0 && i < ACH) load_a1(ka, i);
-          if (c == 0 && i == ACH) load_b1(nxt[0], kb, 0);
-          if ((i & 1) == 0) {
-            if (c < 3)
-              dq(cur[0], c + 1, i >> 1, bf[n][0]);
-            else
-              dq(nxt[0], 0, i >> 1, bf[n][0]);
-          }
-          if (c == 3 && i < ACH) *a_dst(b2, i) = ar[i];
-          __builtin_amdgcn_sched_barrier(0);
-        }
-      }
-      __syncthreads();
-      abuf = b1;
-      return;
-    }
-#pragma unroll
-    for (int c = 0; c < 4; ++c) {
-      const int p = c & 1, n = p ^ 1;
-#pragma unroll
-      for (int i = 0; i < TI; ++i)
-#pragma unroll
-        for (int j = 0; j < TJ; ++j) {
-          const int mi = i * TJ + j;
-          acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(af[p][i], bf[p][j], acc[i][j], 0, 0, 0);
-          if (c == 0 && mi < ACH) load_a1(ka, mi);
-          if (c == 0 && mi >= ACH && mi < ACH + TJ) load_b1(nxt[mi - ACH], kb, mi - ACH);
-          if (mi < TI) af[n][mi] = read_a(c < 3 ? abuf : b1, c < 3 ? c + 1 : 0, mi);
-          if (c < 3)
-            dq(cur[mi >> 2], c + 1, mi & 3, bf[n][mi >> 2]);
-          else
-            dq(nxt[mi >> 2], 0, mi & 3, bf[n][mi >> 2]);
-          if (c == 3 && mi >= TI && mi < TI + ACH) *a_dst(b2, mi - TI) = ar[mi - TI];
-          __builtin_amdgcn_sched_barrier(0);
-        }
-    }
-    __syncthreads();
-    abuf = b1;
-  };
+  for (int sub = 0; sub < 4; ++sub) dq(wr0, 0, sub, bf[0]);
 
   // Pairs of steps with one loop exit (the weight stages alternate); an odd
   // last step runs after the loop.
@@ -1073,8 +1033,8 @@ void k_gemm_bf(const GemmDesc d) {
   }
   if (kt < KT) step(kt, wr0, wr1);
 
-  store_tile<EPI, TI, TJ>(d, acc, reinterpret_cast<float*>(smem), wave, lane, m0 + wm * (BF_BM / WMW),
-                          SWI ? tn * HB + wn * (HB / WNW) : tn * BF_BN + wn * (BF_BN / WNW));
+  store_tile<EPI, TI, TJ>(d, acc, reinterpret_cast<float*>(smem), wave, lane, m0,
+                          SWI ? tn * HB + wave * 16 : tn * BF_BN + wave * 32);
 }
 
 // ---------------------------------------------------------------------------
@@ -1316,19 +1276,18 @@ void run_gemm_dma(const GemmDesc& d, hipStream_t s) {
   check_hip(hipGetLastError(), "k_gemm_dma launch");
 }
 
-template <int WT, int EPI, int NWV, int WMW>
+template <int WT, int EPI>
 void run_gemm_bf(const GemmDesc& d, hipStream_t s) {
   const int hb = EPI == EPI_SWIGLU_F16 ? BF_BN / 2 : BF_BN;
-  const int tiles_n = (d.N + hb - 1) / hb;
-  const int tiles_m = (d.M + BF_BM - 1) / BF_BM;
-  static bool attr_set = false;
+  const int n_tiles = ((d.N + hb - 1) / hb) * ((d.M + BF_BM - 1) / BF_BM);
+  static bool attr_set = false;  // per instantiation
   if (!attr_set) {
-    check_hip(hipFuncSetAttribute(reinterpret_cast<const void*>(&k_gemm_bf<WT, EPI, NWV, WMW>),
+    check_hip(hipFuncSetAttribute(reinterpret_cast<const void*>(&k_gemm_bf<WT, EPI>),
                                   hipFuncAttributeMaxDynamicSharedMemorySize, BF_LDS),
               "hipFuncSetAttribute(k_gemm_bf)");
     attr_set = true;
   }
-  hipLaunchKernelGGL((k_gemm_bf<WT, EPI, NWV, WMW>), dim3(tiles_m * tiles_n), dim3(64 * NWV), BF_LDS, s, d);
+  hipLaunchKernelGGL((k_gemm_bf<WT, EPI>), dim3(n_tiles), dim3(64 * BF_NW), BF_LDS, s, d);
   check_hip(hipGetLastError(), "k_gemm_bf launch");
 }
 
@@ -1348,12 +1307,7 @@ void run_gemm_tiled(const GemmDesc& d, int tile, hipStream_t s) {
   }
   if constexpr (!A32 && K64 && WT != T0H_F16) {
     if (tile == 4 && dma_ok(d)) return run_gemm_dma<WT, EPI>(d, s);
-    if (tile == 5) {
-      if constexpr (EPI == EPI_SWIGLU_F16) return run_gemm_bf<WT, EPI, 8, 2>(d, s);
-      else return run_gemm_bf<WT, EPI, 8, 1>(d, s);
-    }
-    if (tile == 6) return run_gemm_bf<WT, EPI, 8, 2>(d, s);
-    if (tile == 7) return run_gemm_bf<WT, EPI, 4, 2>(d, s);
+    if (tile == 5) return run_gemm_bf<WT, EPI>(d, s);
   }
   if constexpr (!A32 && K64) {
     if (tile == 3 || tile == 4) return run_gemm<WT, A32, EPI, K64, 4, 4>(d, s);
