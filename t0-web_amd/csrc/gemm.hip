@@ -219,10 +219,30 @@ __device__ __forceinline__ void store_tile(const GemmDesc& d, floatx16 (&acc)[TI
     b1[j] = (SWI && ok) ? d.bias[N + col] : 0.0f;
   }
   const bool vec_ok = (d.ldy & 3) == 0 && (N & 3) == 0;
+  // Residual: the old values of a 32-row slice are loaded one slice ahead, so
+  // the read-modify-writes do not wait on a memory round trip each.
+  // (Wide waves, NT > 8, load each slice's own values before staging it.)
+  constexpr int NT = W / 8;  // 16-byte chunks per lane per slice
+  constexpr bool RES = EPI == EPI_RESID_F32, RES2 = RES && NT <= 8;
+  float4 yo[RES2 ? 2 : 1][RES ? NT : 1];
+  auto load_old = [&](int i, float4 (&dst)[RES ? NT : 1]) {
+    if constexpr (RES) {
+#pragma unroll
+      for (int t = 0; t < NT; ++t) {
+        const int idx = t * 64 + lane, row = row_base + i * 32 + idx / (W / 4), col = cbase + (idx % (W / 4)) * 4;
+        dst[t] = row < M && col < N ? *reinterpret_cast<const float4*>(static_cast<const float*>(d.y) +
+                                                                       (size_t)row * d.ldy + col)
+                                    : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+      }
+    }
+  };
+  if (RES2 && vec_ok) load_old(0, yo[0]);
   // Each wave stages into and reads back from its own region, and a wave's
   // LDS operations complete in order: no barrier is needed.
 #pragma unroll
   for (int i = 0; i < TI; ++i) {
+    if (RES2 && vec_ok && i + 1 < TI) load_old(i + 1, yo[(i + 1) & 1]);
+    if (RES && !RES2 && vec_ok) load_old(i, yo[0]);
     if constexpr (PAIR) {
       // Results e and e+1 swap across the 16-lane rows: rows 0/2 (gate lanes)
       // end with (gate, up) of result e, rows 1/3 (up lanes) with those of
@@ -262,10 +282,10 @@ __device__ __forceinline__ void store_tile(const GemmDesc& d, floatx16 (&acc)[TI
         if ((EPI == EPI_STORE_F32 || EPI == EPI_STORE_F16) && d.relu) {
           v.x = fmaxf(v.x, 0.0f); v.y = fmaxf(v.y, 0.0f); v.z = fmaxf(v.z, 0.0f); v.w = fmaxf(v.w, 0.0f);
         }
-        if (EPI == EPI_RESID_F32) {
-          float4* y = reinterpret_cast<float4*>(static_cast<float*>(d.y) + o);
-          const float4 old = *y;
-          *y = make_float4(old.x + v.x, old.y + v.y, old.z + v.z, old.w + v.w);
+        if constexpr (RES) {
+          const float4 old = yo[RES2 ? (i & 1) : 0][t];
+          *reinterpret_cast<float4*>(static_cast<float*>(d.y) + o) =
+              make_float4(old.x + v.x, old.y + v.y, old.z + v.z, old.w + v.w);
         } else if (EPI == EPI_STORE_F32) {
           *reinterpret_cast<float4*>(static_cast<float*>(d.y) + o) = v;
         } else {
@@ -1294,16 +1314,14 @@ void run_gemm_bf(const GemmDesc& d, hipStream_t s) {
 template <int WT, bool A32, int EPI, bool K64>
 void run_gemm_tiled(const GemmDesc& d, int tile, hipStream_t s) {
   // By shape (tile 0).  Measured at the config-4 layer shapes (M = 50,688,
-  // Q4_0): the register-operand 256x256 kernel takes the wide outputs (QKV
-  // N = 2304: 239 us vs 290 us for 128x128; SwiGLU N = 2048: 393 us vs
-  // 430 us); at N = 768 its 3 column tiles leave the last of ~2.3 rounds of
-  // workgroups mostly idle, and 128x128 at two workgroups per CU is as fast
-  // (wO) or faster (w2: 253 us vs 265 us).  The DMA and plain 256x256 tiles
-  // lose at every shape.
+  // Q4_0, register-operand 256x256 vs 128x128 kernel): SwiGLU 363 vs 430 us,
+  // QKV 243 vs 290 us, wO 103 vs 107 us, w2 232 vs 238 us.
+  // The DMA and plain 256x256 tiles lose at every shape.  Below ~1024 rows a
+  // 256-row tile is mostly padding.
   if (tile == 0) {
     tile = 1;
     if constexpr (!A32 && K64 && WT != T0H_F16)
-      if (d.M >= 1024 && (EPI == EPI_SWIGLU_F16 || d.N >= 1536)) tile = 5;
+      if (d.M >= 1024) tile = 5;
   }
   if constexpr (!A32 && K64 && WT != T0H_F16) {
     if (tile == 4 && dma_ok(d)) return run_gemm_dma<WT, EPI>(d, s);
