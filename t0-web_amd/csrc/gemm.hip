@@ -868,23 +868,31 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1))) voi
 //    beyond a few instructions per MFMA adds to the MFMA time instead of
 //    overlapping it, and bursts of loads right after a barrier stall issue.
 // ---------------------------------------------------------------------------
-constexpr int BF_BM = 256, BF_BN = 256, BF_NW = 8;
-constexpr int BF_ABUF = BF_BM * LDK;    // halves per activation buffer
-constexpr int BF_LDS = 3 * BF_ABUF * 2;  // 110,592 bytes
+constexpr int BF_BM = 256;
+constexpr int BF_ABUF = BF_BM * LDK;  // halves per activation buffer
+// NWV waves of 32 weight columns each; 8 waves: three activation buffers
+// (110,592 bytes, one workgroup per CU), 4 waves: two (73,728 bytes, two
+// workgroups per CU, so one's epilogue overlaps the other's main loop).
+template <int NWV>
+struct BfCfg {
+  static constexpr int BN = 32 * NWV, NBUF = NWV == 8 ? 3 : 2, LDS = NBUF * BF_ABUF * 2;
+};
 
-template <int WT, int EPI>
-__global__ __launch_bounds__(64 * BF_NW) __attribute__((amdgpu_waves_per_eu(2, 2))) void k_gemm_bf(const GemmDesc d) {
+template <int WT, int EPI, int NWV>
+__global__ __launch_bounds__(64 * NWV) __attribute__((amdgpu_waves_per_eu(2, 2))) void k_gemm_bf(const GemmDesc d) {
+  using C = BfCfg<NWV>;
+  constexpr int BN = C::BN, NBUF = C::NBUF;
   constexpr int TI = BF_BM / 32, TJ = 1;      // 32x32 tiles per wave
-  constexpr int ACH = 2048 / (64 * BF_NW);    // 16-byte activation chunks per thread and step (4)
+  constexpr int ACH = 2048 / (64 * NWV);      // 16-byte activation chunks per thread and step
   constexpr int AQS = BF_BM / ACH;            // row stride between a thread's chunks
   constexpr int NMI = 4 * TI;                 // MFMAs per step
   constexpr int RING = 8, RD = 6;             // A fragment ring; RING divides NMI
   constexpr bool SWI = EPI == EPI_SWIGLU_F16;
-  constexpr int HB = SWI ? BF_BN / 2 : BF_BN;    // output columns per tile
+  constexpr int HB = SWI ? BN / 2 : BN;          // output columns per tile
   constexpr int NWD = WT == T0H_Q8_0 ? 9 : 5;    // raw dwords a lane needs per step
   constexpr int SWD = WT == T0H_Q8_0 ? 17 : 9;   // dwords of one row's two blocks (one step)
-  static_assert(NMI % RING == 0 && RD < RING && ACH < TI, "step work placement");
-  static_assert(BF_NW * 32 * ((SWI ? 16 : 32) + 4) * 4 <= BF_LDS, "epilogue stage fits the LDS");
+  static_assert(NMI % RING == 0 && RD < RING && ACH < NMI && ACH <= TI, "step work placement");
+  static_assert(NWV * 32 * ((SWI ? 16 : 32) + 4) * 4 <= C::LDS, "epilogue stage fits the LDS");
   extern __shared__ __align__(16) _Float16 smem[];
 
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6, h = lane >> 5, lc = lane & 31;
@@ -916,7 +924,7 @@ __global__ __launch_bounds__(64 * BF_NW) __attribute__((amdgpu_waves_per_eu(2, 2
       ok = g < N;
       wrow = lc < 16 ? g : N + g;
     } else {
-      wrow = tn * BF_BN + wave * 32 + lc;
+      wrow = tn * BN + wave * 32 + lc;
       ok = wrow < N;
     }
     woff = (ok ? wrow : 0) * ((K / 32) * block_bytes(WT) / 4) + h * (NWD - 1);
@@ -994,12 +1002,18 @@ __global__ __launch_bounds__(64 * BF_NW) __attribute__((amdgpu_waves_per_eu(2, 2
 
   int abuf = 0;
   // One step: slice c, MFMA i (m = c*TI + i): the ring read of fragment
-  // m + RD (in step kt+1 once past the step), B sub-steps after every other
-  // MFMA, the A(kt+2) chunk loads and the W(kt+1) load in the first slice,
-  // the A(kt+2) stores in the last.
+  // m + RD (with three buffers, in step kt+1 once past the step: its buffer
+  // is complete; with two, the next step reads its first RD fragments after
+  // the barrier), B sub-steps after every other MFMA, the activation chunk
+  // loads of step kt+NBUF-1 after the first ACH MFMAs and the W(kt+1) load
+  // after the next, the activation stores in the last slice.
   auto step = [&](int kt, uint32_t (&cur)[NWD], uint32_t (&nxt)[NWD]) {
-    const int b1 = abuf == 2 ? 0 : abuf + 1, b2 = b1 == 2 ? 0 : b1 + 1;
-    const int kb = min(kt + 1, last), ka = min(kt + 2, last);
+    const int b1 = abuf + 1 == NBUF ? 0 : abuf + 1, b2 = b1 + 1 == NBUF ? 0 : b1 + 1;
+    const int kb = min(kt + 1, last), ka = min(kt + NBUF - 1, last);
+    if constexpr (NBUF == 2) {
+#pragma unroll
+      for (int m = 0; m < RD; ++m) ring[m] = read_a(abuf, m / TI, m % TI);
+    }
 #pragma unroll
     for (int c = 0; c < 4; ++c) {
       const int p = c & 1, n = p ^ 1;
@@ -1007,16 +1021,19 @@ __global__ __launch_bounds__(64 * BF_NW) __attribute__((amdgpu_waves_per_eu(2, 2
       for (int i = 0; i < TI; ++i) {
         const int m = c * TI + i, mr = m + RD;
         acc[i][0] = __builtin_amdgcn_mfma_f32_32x32x16_f16(ring[m % RING], bf[p], acc[i][0], 0, 0, 0);
-        ring[mr % RING] = mr < NMI ? read_a(abuf, mr / TI, mr % TI) : read_a(b1, 0, mr - NMI);
-        if (c == 0 && i < ACH) load_a(ar[i], ka, i);
-        if (c == 0 && i == ACH) load_b(nxt, kb);
+        if (mr < NMI)
+          ring[mr % RING] = read_a(abuf, mr / TI, mr % TI);
+        else if (NBUF == 3)
+          ring[mr % RING] = read_a(b1, 0, mr - NMI);
+        if (m < ACH) load_a(ar[m], ka, m);
+        if (m == ACH) load_b(nxt, kb);
         if ((i & 1) == 0) {
           if (c < 3)
             dq(cur, c + 1, i >> 1, bf[n]);
           else
             dq(nxt, 0, i >> 1, bf[n]);
         }
-        if (c == 3 && i < ACH) *a_dst(b2, i) = ar[i];
+        if (c == 3 && i < ACH) *a_dst(NBUF == 3 ? b2 : b1, i) = ar[i];
         __builtin_amdgcn_sched_barrier(0);
       }
     }
@@ -1024,23 +1041,29 @@ __global__ __launch_bounds__(64 * BF_NW) __attribute__((amdgpu_waves_per_eu(2, 2
     abuf = b1;
   };
 
-  // Prologue: A(0), A(1) into buffers 0 and 1, W(0), the first ring
-  // fragments and the slice-0 B fragment.
+  // Prologue: A(0) (and, with three buffers, A(1)) into the first buffers,
+  // W(0), the first ring fragments and the slice-0 B fragment.
   {
     u32x4 ar1[ACH];
 #pragma unroll
     for (int q = 0; q < ACH; ++q) load_a(ar[q], 0, q);
+    if constexpr (NBUF == 3) {
 #pragma unroll
-    for (int q = 0; q < ACH; ++q) load_a(ar1[q], min(1, last), q);
+      for (int q = 0; q < ACH; ++q) load_a(ar1[q], min(1, last), q);
+    }
     load_b(wr0, 0);
 #pragma unroll
     for (int q = 0; q < ACH; ++q) *a_dst(0, q) = ar[q];
+    if constexpr (NBUF == 3) {
 #pragma unroll
-    for (int q = 0; q < ACH; ++q) *a_dst(1, q) = ar1[q];
+      for (int q = 0; q < ACH; ++q) *a_dst(1, q) = ar1[q];
+    }
   }
   __syncthreads();
+  if constexpr (NBUF == 3) {
 #pragma unroll
-  for (int m = 0; m < RD; ++m) ring[m] = read_a(0, m / TI, m % TI);
+    for (int m = 0; m < RD; ++m) ring[m] = read_a(0, m / TI, m % TI);
+  }
 #pragma unroll
   for (int sub = 0; sub < 4; ++sub) dq(wr0, 0, sub, bf[0]);
 
@@ -1054,7 +1077,7 @@ __global__ __launch_bounds__(64 * BF_NW) __attribute__((amdgpu_waves_per_eu(2, 2
   if (kt < KT) step(kt, wr0, wr1);
 
   store_tile<EPI, TI, TJ>(d, acc, reinterpret_cast<float*>(smem), wave, lane, m0,
-                          SWI ? tn * HB + wave * 16 : tn * BF_BN + wave * 32);
+                          SWI ? tn * HB + wave * 16 : tn * BN + wave * 32);
 }
 
 // ---------------------------------------------------------------------------
@@ -1296,36 +1319,38 @@ void run_gemm_dma(const GemmDesc& d, hipStream_t s) {
   check_hip(hipGetLastError(), "k_gemm_dma launch");
 }
 
-template <int WT, int EPI>
+template <int WT, int EPI, int NWV>
 void run_gemm_bf(const GemmDesc& d, hipStream_t s) {
-  const int hb = EPI == EPI_SWIGLU_F16 ? BF_BN / 2 : BF_BN;
+  using C = BfCfg<NWV>;
+  const int hb = EPI == EPI_SWIGLU_F16 ? C::BN / 2 : C::BN;
   const int n_tiles = ((d.N + hb - 1) / hb) * ((d.M + BF_BM - 1) / BF_BM);
   static bool attr_set = false;  // per instantiation
   if (!attr_set) {
-    check_hip(hipFuncSetAttribute(reinterpret_cast<const void*>(&k_gemm_bf<WT, EPI>),
-                                  hipFuncAttributeMaxDynamicSharedMemorySize, BF_LDS),
+    check_hip(hipFuncSetAttribute(reinterpret_cast<const void*>(&k_gemm_bf<WT, EPI, NWV>),
+                                  hipFuncAttributeMaxDynamicSharedMemorySize, C::LDS),
               "hipFuncSetAttribute(k_gemm_bf)");
     attr_set = true;
   }
-  hipLaunchKernelGGL((k_gemm_bf<WT, EPI>), dim3(n_tiles), dim3(64 * BF_NW), BF_LDS, s, d);
+  hipLaunchKernelGGL((k_gemm_bf<WT, EPI, NWV>), dim3(n_tiles), dim3(64 * NWV), C::LDS, s, d);
   check_hip(hipGetLastError(), "k_gemm_bf launch");
 }
 
 template <int WT, bool A32, int EPI, bool K64>
 void run_gemm_tiled(const GemmDesc& d, int tile, hipStream_t s) {
   // By shape (tile 0).  Measured at the config-4 layer shapes (M = 50,688,
-  // Q4_0, register-operand 256x256 vs 128x128 kernel): SwiGLU 363 vs 430 us,
-  // QKV 243 vs 290 us, wO 103 vs 107 us, w2 232 vs 238 us.
-  // The DMA and plain 256x256 tiles lose at every shape.  Below ~1024 rows a
-  // 256-row tile is mostly padding.
+  // Q4_0, us; register-operand 256x128 at two workgroups per CU / 256x256 /
+  // 128x128): SwiGLU 360 / 363 / 430, QKV 250 / 245 / 290, wO 97 / 103 / 107,
+  // w2 224 / 232 / 238.  The DMA and plain 256x256 tiles lose at every shape.
+  // Below ~1024 rows a 256-row tile is mostly padding.
   if (tile == 0) {
     tile = 1;
     if constexpr (!A32 && K64 && WT != T0H_F16)
-      if (d.M >= 1024) tile = 5;
+      if (d.M >= 1024) tile = EPI != EPI_SWIGLU_F16 && d.N >= 1536 ? 5 : 6;
   }
   if constexpr (!A32 && K64 && WT != T0H_F16) {
     if (tile == 4 && dma_ok(d)) return run_gemm_dma<WT, EPI>(d, s);
-    if (tile == 5) return run_gemm_bf<WT, EPI>(d, s);
+    if (tile == 5) return run_gemm_bf<WT, EPI, 8>(d, s);
+    if (tile == 6) return run_gemm_bf<WT, EPI, 4>(d, s);
   }
   if constexpr (!A32 && K64) {
     if (tile == 3 || tile == 4) return run_gemm<WT, A32, EPI, K64, 4, 4>(d, s);
