@@ -175,7 +175,8 @@ def traffic_of(kind, quant):
         rec = json.load(open(TRAFFIC_FILE))
     except (OSError, ValueError):
         return None
-    return rec.get("traffic") if (rec.get("kind"), rec.get("quant")) == (kind, quant) else None
+    same = (rec.get("kind"), rec.get("quant"), rec.get("kernel")) == (kind, quant, KERNEL_OF.get((kind, quant)))
+    return rec.get("traffic") if same else None
 
 
 def summarize(prof_dir, fetch_dir, write_dir, quant, kind):
@@ -193,7 +194,7 @@ def summarize(prof_dir, fetch_dir, write_dir, quant, kind):
         for r in rows[:16]:
             lines.append(f"| `{r['Name'][:110]}` | {r['Calls']} | {float(r['TotalDurationNs']) / 1e3:.1f} | "
                          f"{float(r['AverageNs']) / 1e3:.2f} | {float(r['Percentage']):.2f} |")
-    res = {"kind": kind, "quant": quant}
+    res = {"kind": kind, "quant": quant, "kernel": KERNEL_OF[(kind, quant)]}
     for ctr, d in (("FETCH_SIZE", fetch_dir), ("WRITE_SIZE", write_dir)):
         disp = _pmc_per_dispatch(d)
         copies = [v for (n, g, v) in disp.values() if "copyBuffer" in n and v * 1024 > COPY_BYTES / 4]
