@@ -6,6 +6,7 @@
 #include <string>
 
 #include "kernels.h"
+#include "lanes.h"
 #include "t0hip_internal.h"
 
 namespace t0h {
@@ -39,6 +40,37 @@ __global__ __launch_bounds__(256) void k_rmsnorm(const float* x, const float* sc
     const half4 h = {(_Float16)((v.x / denom) * s.x), (_Float16)((v.y / denom) * s.y), (_Float16)((v.z / denom) * s.z),
                      (_Float16)((v.w / denom) * s.w)};
     *reinterpret_cast<half4*>(dst + c) = h;
+  }
+}
+
+// Rows up to 1024 wide: the wave holds its row in registers (one memory round
+// trip), sums over DPP lane moves and row swaps, normalizes from registers.
+__global__ __launch_bounds__(256) void k_rmsnorm_reg(const float* x, const float* scale, _Float16* out,
+                                                     const int* map, int rows, int dim) {
+  const int lane = threadIdx.x & 63;
+  const int row = blockIdx.x * 4 + (threadIdx.x >> 6);
+  if (row >= rows) return;
+  const float* src = x + (size_t)(map ? map[row] : row) * dim;
+  float4 v[4];
+  float ss = 0.0f;
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+    const int c = lane * 4 + j * 256;
+    v[j] = c < dim ? *reinterpret_cast<const float4*>(src + c) : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+    ss += v[j].x * v[j].x + v[j].y * v[j].y + v[j].z * v[j].z + v[j].w * v[j].w;
+  }
+  ss = rows_sum(lane_sum16(ss));
+  const float denom = sqrtf(ss / (float)dim + 1e-8f);
+  _Float16* dst = out + (size_t)row * dim;
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+    const int c = lane * 4 + j * 256;
+    if (c < dim) {
+      const float4 s = *reinterpret_cast<const float4*>(scale + c);
+      const half4 h = {(_Float16)((v[j].x / denom) * s.x), (_Float16)((v[j].y / denom) * s.y),
+                       (_Float16)((v[j].z / denom) * s.z), (_Float16)((v[j].w / denom) * s.w)};
+      *reinterpret_cast<half4*>(dst + c) = h;
+    }
   }
 }
 
@@ -318,7 +350,10 @@ void launch_rmsnorm(const float* x, const float* scale, _Float16* out, const int
   if (rows <= 0) return;
   if (!x || !scale || !out) throw Error(T0H_ERR_INVALID_ARG, "rmsnorm: null pointer");
   if (dim <= 0 || dim % 4) throw Error(T0H_ERR_UNSUPPORTED, "rmsnorm: dim must be a positive multiple of 4");
-  hipLaunchKernelGGL(k_rmsnorm, dim3(blocks(rows, 4)), dim3(256), 0, s, x, scale, out, row_map, rows, dim);
+  if (dim <= 1024)
+    hipLaunchKernelGGL(k_rmsnorm_reg, dim3(blocks(rows, 4)), dim3(256), 0, s, x, scale, out, row_map, rows, dim);
+  else
+    hipLaunchKernelGGL(k_rmsnorm, dim3(blocks(rows, 4)), dim3(256), 0, s, x, scale, out, row_map, rows, dim);
   check_hip(hipGetLastError(), "k_rmsnorm launch");
 }
 
