@@ -891,7 +891,7 @@ __global__ __launch_bounds__(64 * NWV) __attribute__((amdgpu_waves_per_eu(2, 2))
   constexpr int HB = SWI ? BN / 2 : BN;          // output columns per tile
   constexpr int NWD = WT == T0H_Q8_0 ? 9 : 5;    // raw dwords a lane needs per step
   constexpr int SWD = WT == T0H_Q8_0 ? 17 : 9;   // dwords of one row's two blocks (one step)
-  static_assert(NMI % RING == 0 && RD < RING && ACH < NMI && ACH <= TI, "step work placement");
+  static_assert(NMI % RING == 0 && RD < RING && ACH <= TI, "step work placement");
   static_assert(NWV * 32 * ((SWI ? 16 : 32) + 4) * 4 <= C::LDS, "epilogue stage fits the LDS");
   extern __shared__ __align__(16) _Float16 smem[];
 
@@ -1005,8 +1005,11 @@ __global__ __launch_bounds__(64 * NWV) __attribute__((amdgpu_waves_per_eu(2, 2))
   // m + RD (with three buffers, in step kt+1 once past the step: its buffer
   // is complete; with two, the next step reads its first RD fragments after
   // the barrier), B sub-steps after every other MFMA, the activation chunk
-  // loads of step kt+NBUF-1 after the first ACH MFMAs and the W(kt+1) load
-  // after the next, the activation stores in the last slice.
+  // loads of step kt+NBUF-1 and the W(kt+1) load early in the first slices
+  // (W first when the ACH = 8 chunk loads would push it into the second
+  // slice: its data is needed in the last), the activation stores in the
+  // last slice.
+  constexpr int WPOS = ACH < TI ? ACH : 0, A0 = ACH < TI ? 0 : 1;
   auto step = [&](int kt, uint32_t (&cur)[NWD], uint32_t (&nxt)[NWD]) {
     const int b1 = abuf + 1 == NBUF ? 0 : abuf + 1, b2 = b1 + 1 == NBUF ? 0 : b1 + 1;
     const int kb = min(kt + 1, last), ka = min(kt + NBUF - 1, last);
@@ -1025,8 +1028,8 @@ __global__ __launch_bounds__(64 * NWV) __attribute__((amdgpu_waves_per_eu(2, 2))
           ring[mr % RING] = read_a(abuf, mr / TI, mr % TI);
         else if (NBUF == 3)
           ring[mr % RING] = read_a(b1, 0, mr - NMI);
-        if (m < ACH) load_a(ar[m], ka, m);
-        if (m == ACH) load_b(nxt, kb);
+        if (m == WPOS) load_b(nxt, kb);
+        if (m >= A0 && m < A0 + ACH) load_a(ar[m - A0], ka, m - A0);
         if ((i & 1) == 0) {
           if (c < 3)
             dq(cur, c + 1, i >> 1, bf[n]);
