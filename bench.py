@@ -16,7 +16,10 @@ Also reported on the same JSON line:
   gemm_sweep    BASELINE configs 1-2: the kernel-level Q-GEMM (f32 in/out) at
                 M in {1,16,64,512,8192} x (K,N) shapes, TFLOP/s and GB/s;
                 small-M cases rotate through >256 MB of weight copies so the
-                Infinity Cache cannot serve them.
+                Infinity Cache cannot serve them;
+  workloads     BASELINE config 3 (one series, latency) and config 5 (64 x 8
+                autoregressive rollout, Q8_0) through the host-buffer entry
+                points, with the oracle on a bounded sample beside each.
 """
 import argparse
 import json
@@ -57,6 +60,83 @@ def config4_inputs(n_series=256, n_var=3, t_ctx=2048, seed=0):
             x[r, s:s + L] = np.nan
     groups = np.repeat(np.arange(n_series), n_var).astype(np.int64)
     return x.astype(np.float32), groups
+
+
+def config3_input(t_ctx=2048, seed=3):
+    """One univariate series: sum of 3 sines (periods U[7,365]) + N(0, 0.1) noise."""
+    rng = np.random.default_rng(seed)
+    tt = np.arange(t_ctx, dtype=np.float64)
+    x = sum(np.sin(2 * np.pi * tt / rng.uniform(7, 365) + rng.uniform(0, 2 * np.pi)) for _ in range(3))
+    return (x + 0.1 * rng.standard_normal(t_ctx)).astype(np.float32)
+
+
+def config5_inputs(n_series=64, n_var=8, t_ctx=4096, seed=5):
+    """Linear trend + daily and weekly seasonal terms + Student-t(3) noise per row."""
+    rng = np.random.default_rng(seed)
+    rows = n_series * n_var
+    tt = np.arange(t_ctx, dtype=np.float64)
+    x = rng.normal(0.0, 5.0, (rows, 1)) + rng.normal(0.0, 0.01, (rows, 1)) * tt
+    for period in (24.0, 168.0):
+        x = x + rng.uniform(0.5, 3.0, (rows, 1)) * np.sin(2 * np.pi * tt / period + rng.uniform(0, 2 * np.pi, (rows, 1)))
+    x += 0.3 * rng.standard_t(3, (rows, t_ctx))
+    return x.astype(np.float32), np.repeat(np.arange(n_series), n_var).astype(np.int64)
+
+
+def median_time(fn, reps):
+    ts = []
+    for _ in range(reps):
+        t = time.perf_counter()
+        fn()
+        ts.append(time.perf_counter() - t)
+    return float(np.median(ts))
+
+
+def other_workloads(torch, t0hip, engine, cfg, with_cpu, reps=5):
+    """BASELINE configs 3 and 5 through the host-buffer entry points (upload of the context and
+    download of the result included, as the reference's own bench times them), median of `reps`
+    after one warm-up; the oracle beside each on a bounded sample when `with_cpu`."""
+    res = {}
+    gguf = t0hip.synth_model_gguf(cfg, quant=t0hip.Q8_0, seed=0)
+    model = t0hip.load_model_from_gguf(engine, gguf)
+    om = None
+    if with_cpu:
+        sys.path.insert(0, os.path.join(ROOT, "oracle"))
+        import t0ref  # the CPU checker/baseline, test infrastructure
+        om = t0ref.Model(gguf)
+
+    x3 = config3_input()
+    run3 = lambda: t0hip.forecast(engine, model, x3, 1, x3.size, 64)
+    run3()
+    ms3 = median_time(run3, 4 * reps) * 1e3
+    res["config3"] = {"workload": "1 series, sum of 3 sines + N(0,0.1), ctx 2048, horizon 64, Q8_0",
+                      "ms_per_forecast": round(ms3, 3), "gemm_rows": 66}
+    if om is not None:
+        om.forecast(x3, 1, x3.size, 64)
+        res["config3"]["cpu_ms_per_forecast"] = round(median_time(lambda: om.forecast(x3, 1, x3.size, 64), 3) * 1e3, 1)
+    log(f"config 3: {ms3:.3f} ms per forecast")
+
+    x5, g5 = config5_inputs()
+    t_ctx, h, steps = x5.shape[1], 64, 8
+    run5 = lambda: t0hip.forecast_grouped_ar(engine, model, x5, g5, t_ctx, h, steps)
+    run5()
+    s5 = median_time(run5, reps)
+    p5 = (t_ctx + h + 31) // 32
+    flops = 2.0 * x5.shape[0] * p5 * 7077888 * cfg.num_layers * steps
+    res["config5"] = {"workload": "64 series x 8 variates, trend + seasonality + Student-t(3), ctx 4096, "
+                                  "8 AR steps of horizon 64, Q8_0, weights resident across steps",
+                      "ms_per_rollout": round(s5 * 1e3, 2), "series_rollouts_per_s": round(64 / s5, 2),
+                      "gemm_rows_per_step": x5.shape[0] * p5,
+                      "layer_gemm_tflops_effective": round(flops / s5 * 1e-12, 1)}
+    if om is not None:
+        # one series (8 variates), 2 of the 8 AR steps
+        t = time.perf_counter()
+        om.forecast_grouped_ar(x5[:8], g5[:8], t_ctx, h, 2)
+        dt = time.perf_counter() - t
+        res["config5"]["cpu_sample"] = {"series_rollouts_per_s": round(2 / steps / dt, 4),
+                                        "sample": f"1 series x 8 variates, 2 of 8 AR steps, {dt:.1f} s"}
+    log(f"config 5: {s5 * 1e3:.1f} ms per rollout")
+    model.close()
+    return res
 
 
 def gemm_flops(name, M, cfg):
@@ -235,6 +315,7 @@ def main():
     ap.add_argument("--profile-steps", type=int, default=5)
     ap.add_argument("--no-sweep", action="store_true")
     ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--no-workloads", action="store_true", help="skip BASELINE configs 3 and 5")
     ap.add_argument("--quant", default="q4_0", choices=["q4_0", "q8_0"])
     ap.add_argument("--calibrate-copy", action="store_true",
                     help="first run one plain 256 MiB device-to-device copy (reference for PMC byte counters)")
@@ -321,6 +402,10 @@ def main():
     if not args.no_sweep:
         log("GEMM sweep (configs 1-2)")
         sweep = gemm_sweep(torch, t0hip)
+    workloads = None
+    if not args.no_workloads:
+        log("BASELINE configs 3 and 5")
+        workloads = other_workloads(torch, t0hip, engine, cfg, not args.no_cpu)
     cpu = None
     if not args.no_cpu:
         log("CPU baseline (oracle)")
@@ -341,6 +426,7 @@ def main():
         "host_buffers_forecasts_per_s": round(host_rate, 2),
         "kernels": kernels,
         "gemm_sweep": sweep,
+        "workloads": workloads,
     }
     print(json.dumps(line), flush=True)
 
