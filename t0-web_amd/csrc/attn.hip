@@ -33,7 +33,7 @@ typedef float floatx4 __attribute__((ext_vector_type(4)));
 
 constexpr int HD = 64;
 constexpr int LDH = HD + 8;
-constexpr int MAXKT = T0H_MAX_PATCHES / 16;
+constexpr int TA_WAVES = 4;
 
 __host__ __device__ inline int round_up(int x, int m) { return (x + m - 1) / m * m; }
 
@@ -42,160 +42,199 @@ __host__ __device__ inline int round_up(int x, int m) { return (x + m - 1) / m *
 // pairs land in distinct banks up to a 2-way conflict.
 __host__ __device__ inline int vt_stride(int P32) { return P32 + 4; }
 
+// LDS of one (row, head) workgroup: Ks [P16][LDH] f16 keys after norm + RoPE
+// (rows >= p zero) | Vt [HD][LDV] f16 values by key pairs (keys >= p zero) |
+// Os [TA_WAVES][16][LDH] per-wave output staging | Kg [P32] int key group if
+// attendable, -2 if not, -4 past the window.
 size_t time_attn_lds(int p) {
   const int P16 = round_up(p, 16), P32 = round_up(p, 32);
-  return (size_t)(P16 + P32) * LDH * 2 + (size_t)HD * vt_stride(P32) * 2 + (size_t)P32 * 4 + (size_t)P32;
+  return (size_t)P16 * LDH * 2 + (size_t)HD * vt_stride(P32) * 2 + (size_t)TA_WAVES * 16 * LDH * 2 + (size_t)P32 * 4;
 }
 
+__device__ __forceinline__ void unpack8(uint4 u, float* x) {
+  const half8 hv = __builtin_bit_cast(half8, u);
+#pragma unroll
+  for (int e = 0; e < 8; ++e) x[e] = (float)hv[e];
+}
 
-// One workgroup per (variate row, head), 4 waves over the 16-query tiles.
-// Load phase: 8 lanes per 64-wide q/k row (16 B each), QK-RMSNorm reduced over
-// the 8-lane group, interleaved xPos RoPE on the lane's 4 adjacent pairs, q/k
-// stored row-major; v rows in key pairs, transposed into
-// LDS as (key 2i, key 2i+1) dwords.  Compute phase: per 16-query tile,
-// S^T = K Q^T and O = P V on v_mfma_f32_16x16x32_f16 with the tile's scores in
-// registers; O is staged through the tile's own Q rows and stored in 16-byte
-// row chunks.
+// Eight adjacent dims (four rotation pairs) of a QK-normalized, rotated row:
+// inv * (x[e] * A[e] + x[e^1] * B[e]) with A at tab[0..7] and B at tab[64..71].
+__device__ __forceinline__ half8 rotate8(const float* x, const float* a, const float* b, float inv) {
+  half8 o;
+#pragma unroll
+  for (int e = 0; e < 8; ++e) o[e] = (_Float16)(((x[e] * inv) * a[e]) + ((x[e ^ 1] * inv) * b[e]));
+  return o;
+}
+
+__device__ __forceinline__ void load_f8(const float* t, float* a) {
+  const float4 u = *reinterpret_cast<const float4*>(t), w = *reinterpret_cast<const float4*>(t + 4);
+  a[0] = u.x, a[1] = u.y, a[2] = u.z, a[3] = u.w, a[4] = w.x, a[5] = w.y, a[6] = w.z, a[7] = w.w;
+}
+
+// One workgroup per (variate row, head), TA_WAVES waves.
+// Key phase: 8 lanes per 64-wide k row (16 B each), QK-RMSNorm reduced over
+// the 8-lane group, norm scale + interleaved xPos RoPE from the folded tables,
+// keys stored row-major; v rows in key pairs, transposed into LDS as
+// (key 2i, key 2i+1) dwords.  Query phase: each wave takes 16-query tiles in a
+// snake order over decreasing causal cost; a tile's queries are loaded straight
+// into the MFMA operand layout (lane: query lane%16, dims 8(lane/16)..+7 and
+// 32 + 8(lane/16)..+7), normalized across the four lanes that hold a query and
+// rotated in registers; S^T = K Q^T and O = P V on v_mfma_f32_16x16x32_f16 with
+// the tile's scores in registers; O is staged through the wave's LDS region and
+// stored in 16-byte row chunks.
 template <int MAXKT>
-__global__ __launch_bounds__(256) void k_time_attn(const AttnDesc d) {
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(MAXKT <= 8 ? 4 : 3))) void k_time_attn(const AttnDesc d) {
   extern __shared__ __align__(16) _Float16 sm[];
   const int p = d.p, P16 = round_up(p, 16), P32 = round_up(p, 32), LDV = vt_stride(P32);
-  _Float16* Qs = sm;
-  _Float16* Ks = Qs + P16 * LDH;
-  _Float16* Vt = Ks + P32 * LDH;
-  int* Gk = reinterpret_cast<int*>(Vt + HD * LDV);
-  uint8_t* Ak = reinterpret_cast<uint8_t*>(Gk + P32);
+  _Float16* Ks = sm;
+  _Float16* Vt = Ks + P16 * LDH;
+  _Float16* Os = Vt + HD * LDV;
+  int* Kg = reinterpret_cast<int*>(Os + TA_WAVES * 16 * LDH);
 
-  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6, nth = blockDim.x, nwaves = nth >> 6;
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6, part = lane >> 4;
   const int r = blockIdx.x / d.heads, h = blockIdx.x % d.heads;
   const int E = d.E, ld = 3 * E;
   const size_t row0 = (size_t)r * p;
+  const _Float16* qb = d.qkv + row0 * ld + h * HD;  // q; k at +E, v at +2E
+  const int nqt = P16 / 16, all_kt = P32 / 16;
 
-  for (int i = tid; i < P32; i += nth) {
-    Gk[i] = i < p ? d.grp[row0 + i] : -2;
-    Ak[i] = i < p ? d.att[row0 + i] : 0;
-  }
-  // Items: q rows, k rows, v key pairs; each 8-lane group takes every 32nd.
-  // All of a thread's global loads are issued before any is consumed.
-  const int n_items = P16 + P32 + P32 / 2;
-  const int d0 = (tid & 7) * 8;
-  constexpr int NIT = (MAXKT * 16 * 5 / 2 + 31) / 32;  // items per group at the largest window
-  uint4 g0[NIT], g1[NIT];
-#pragma unroll
-  for (int it = 0; it < NIT; ++it) {
-    const int item = (tid >> 3) + 32 * it;
-    g0[it] = make_uint4(0, 0, 0, 0);
-    g1[it] = make_uint4(0, 0, 0, 0);
-    if (item >= n_items) continue;
-    int which, i;
-    if (item < P16) {
-      which = 0;
-      i = item;
-    } else if (item < P16 + P32) {
-      which = 1;
-      i = item - P16;
-    } else {
-      which = 2;
-      i = 2 * (item - P16 - P32);
+  // This wave's j-th tile in cost order (the snake over waves); -1 when past the last.
+  auto tile_at = [&](int k) {
+    const int j = (k >> 1) * 2 * TA_WAVES + ((k & 1) ? 2 * TA_WAVES - 1 - wave : wave);
+    return j < nqt ? nqt - 1 - j : -1;
+  };
+  auto load_q = [&](int qt, uint4& a, uint4& b) {
+    const int qi = qt * 16 + (lane & 15);
+    a = b = make_uint4(0, 0, 0, 0);
+    if (qt >= 0 && qi < p) {
+      a = *reinterpret_cast<const uint4*>(qb + (size_t)qi * ld + part * 8);
+      b = *reinterpret_cast<const uint4*>(qb + (size_t)qi * ld + 32 + part * 8);
     }
-    const _Float16* src = d.qkv + (row0 + i) * ld + (size_t)which * E + h * HD + d0;
-    if (i < p) g0[it] = *reinterpret_cast<const uint4*>(src);
-    if (which == 2 && i + 1 < p) g1[it] = *reinterpret_cast<const uint4*>(src + ld);
+  };
+
+  // Key phase: all of a thread's k / v loads are issued before any is consumed.
+  constexpr int NK = MAXKT / 2, NV = MAXKT / 4;  // items per 8-lane group at the largest window
+  const int d0 = (tid & 7) * 8, g8 = tid >> 3;
+  uint4 kx[NK], vx[NV][2];
+#pragma unroll
+  for (int it = 0; it < NK; ++it) {
+    const int i = g8 + 32 * it;
+    kx[it] = i < p ? *reinterpret_cast<const uint4*>(qb + E + (size_t)i * ld + d0) : make_uint4(0, 0, 0, 0);
   }
 #pragma unroll
-  for (int it = 0; it < NIT; ++it) {
-    const int item = (tid >> 3) + 32 * it;
-    if (item >= n_items) break;
-    int which, i;
-    if (item < P16) {
-      which = 0;
-      i = item;
-    } else if (item < P16 + P32) {
-      which = 1;
-      i = item - P16;
-    } else {
-      which = 2;
-      i = 2 * (item - P16 - P32);  // key pair (i, i+1)
-    }
-    const half8 hv = __builtin_bit_cast(half8, g0[it]);
-    if (which == 2) {
-      const half8 hw = __builtin_bit_cast(half8, g1[it]);
-      uint32_t* vt2 = reinterpret_cast<uint32_t*>(Vt);
+  for (int it = 0; it < NV; ++it) {
+    const int i = 2 * (g8 + 32 * it);
+    const _Float16* src = qb + 2 * E + (size_t)i * ld + d0;
+    vx[it][0] = i < p ? *reinterpret_cast<const uint4*>(src) : make_uint4(0, 0, 0, 0);
+    vx[it][1] = i + 1 < p ? *reinterpret_cast<const uint4*>(src + ld) : make_uint4(0, 0, 0, 0);
+  }
+  uint4 qa, qc;
+  load_q(tile_at(0), qa, qc);
+  for (int i = tid; i < P32; i += blockDim.x) Kg[i] = i >= p ? -4 : d.att[row0 + i] ? d.grp[row0 + i] : -2;
 #pragma unroll
-      for (int e = 0; e < 8; ++e) {
-        const half2v pr = {hv[e], hw[e]};
-        vt2[((d0 + e) * LDV + i) >> 1] = __builtin_bit_cast(uint32_t, pr);
-      }
-      continue;
-    }
+  for (int it = 0; it < NK; ++it) {
+    const int i = g8 + 32 * it;
+    if (i >= P16) break;
     float x[8];
+    unpack8(kx[it], x);
     float ss = 0.0f;
 #pragma unroll
-    for (int e = 0; e < 8; ++e) {
-      x[e] = (float)hv[e];
-      ss += x[e] * x[e];
-    }
+    for (int e = 0; e < 8; ++e) ss += x[e] * x[e];
     ss = lane_sum8(ss);
     half8 o = {};
     if (i < p) {
-      const float inv = 1.0f / sqrtf(ss / (float)HD + 1e-8f);
-      const float* nrm = (which ? d.k_norm : d.q_norm) + d0;
-      const float* ct = d.rope_cos + (size_t)i * HD + d0;
-      const float* st = d.rope_sin + (size_t)i * HD + d0;
-      const float* xt = (which ? d.rope_scale_inv : d.rope_scale) + (size_t)i * HD + d0;
-#pragma unroll
-      for (int e = 0; e < 8; ++e) x[e] = (x[e] * inv) * nrm[e];
-#pragma unroll
-      for (int e = 0; e < 8; ++e) {
-        const float rot = (e & 1) ? x[e - 1] : -x[e + 1];
-        o[e] = (_Float16)(((x[e] * ct[e]) * xt[e]) + ((rot * st[e]) * xt[e]));
-      }
+      float a[8], b[8];
+      load_f8(d.rope_k + (size_t)i * 128 + d0, a);
+      load_f8(d.rope_k + (size_t)i * 128 + 64 + d0, b);
+      o = rotate8(x, a, b, 1.0f / sqrtf(ss / (float)HD + 1e-8f));
     }
-    *reinterpret_cast<uint4*>((which ? Ks : Qs) + i * LDH + d0) = __builtin_bit_cast(uint4, o);
+    *reinterpret_cast<uint4*>(Ks + i * LDH + d0) = __builtin_bit_cast(uint4, o);
+  }
+#pragma unroll
+  for (int it = 0; it < NV; ++it) {
+    const int i = 2 * (g8 + 32 * it);
+    if (i >= P32) break;
+    const half8 hv = __builtin_bit_cast(half8, vx[it][0]), hw = __builtin_bit_cast(half8, vx[it][1]);
+    uint32_t* vt2 = reinterpret_cast<uint32_t*>(Vt);
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+      const half2v pr = {hv[e], hw[e]};
+      vt2[((d0 + e) * LDV + i) >> 1] = __builtin_bit_cast(uint32_t, pr);
+    }
   }
   __syncthreads();
 
   const bool fut = d.fut[r] != 0;
-  const int nqt = P16 / 16, all_kt = P32 / 16;
-  for (int qt = wave; qt < nqt; qt += nwaves) {
-    const int q = qt * 16 + (lane & 15);
-    const int gq = q < p ? Gk[q] : -1;
-    const bool need_all = fut || __ballot(q < p && gq < 0) != 0;
+  _Float16* ost = Os + wave * 16 * LDH;
+  for (int k = 0;; ++k) {
+    const int qt = tile_at(k);
+    if (qt < 0) break;
+    const int qi = qt * 16 + (lane & 15);
+    float ta[16], tb[16];
+    if (qi < p) {
+      const float* t = d.rope_q + (size_t)qi * 128 + part * 8;
+      load_f8(t, ta);
+      load_f8(t + 32, ta + 8);
+      load_f8(t + 64, tb);
+      load_f8(t + 96, tb + 8);
+    }
+    uint4 na, nc;  // the next tile's queries, in flight during this tile
+    load_q(tile_at(k + 1), na, nc);
+    float x[16];
+    unpack8(qa, x);
+    unpack8(qc, x + 8);
+    float ss = 0.0f;
+#pragma unroll
+    for (int e = 0; e < 16; ++e) ss += x[e] * x[e];
+    ss = rows_sum(ss);
+    half8 bq0 = {}, bq1 = {};
+    if (qi < p) {
+      const float inv = 1.0f / sqrtf(ss / (float)HD + 1e-8f);
+      bq0 = rotate8(x, ta, tb, inv);
+      bq1 = rotate8(x + 8, ta + 8, tb + 8, inv);
+    }
+    qa = na;
+    qc = nc;
+
+    // A query without a group (an all-PAD patch) has every key blocked; the
+    // reference's softmax then weighs all p keys equally, which a score of 0 on
+    // every key < p gives.  Any other query attends at least itself.
+    const int kq = Kg[qi];
+    const bool blocked = kq < 0;
+    const bool need_all = fut || __ballot(qi < p && blocked) != 0;
     const int nkt = need_all ? all_kt : min(all_kt, (qt + 2) & ~1);
-    const _Float16* qrow = Qs + (qt * 16 + (lane & 15)) * LDH + (lane >> 4) * 8;
-    const half8 bq0 = *reinterpret_cast<const half8*>(qrow);
-    const half8 bq1 = *reinterpret_cast<const half8*>(qrow + 32);
 
     float sc[MAXKT][4];
     float mx = -INFINITY;
 #pragma unroll
     for (int kt = 0; kt < MAXKT; ++kt) {
       if (kt < nkt) {
-        const _Float16* krow = Ks + (kt * 16 + (lane & 15)) * LDH + (lane >> 4) * 8;
         floatx4 s = {0.f, 0.f, 0.f, 0.f};
-        s = __builtin_amdgcn_mfma_f32_16x16x32_f16(*reinterpret_cast<const half8*>(krow), bq0, s, 0, 0, 0);
-        s = __builtin_amdgcn_mfma_f32_16x16x32_f16(*reinterpret_cast<const half8*>(krow + 32), bq1, s, 0, 0, 0);
+        if (kt * 16 < p) {
+          const _Float16* krow = Ks + (kt * 16 + (lane & 15)) * LDH + part * 8;
+          s = __builtin_amdgcn_mfma_f32_16x16x32_f16(*reinterpret_cast<const half8*>(krow), bq0, s, 0, 0, 0);
+          s = __builtin_amdgcn_mfma_f32_16x16x32_f16(*reinterpret_cast<const half8*>(krow + 32), bq1, s, 0, 0, 0);
+        }
+        const int4 kg = *reinterpret_cast<const int4*>(Kg + kt * 16 + part * 4);
+        const int kgv[4] = {kg.x, kg.y, kg.z, kg.w};
+        const int rel = qi - kt * 16 - part * 4;  // key e of this lane is causal iff e <= rel
 #pragma unroll
         for (int e = 0; e < 4; ++e) {
-          const int key = kt * 16 + (lane >> 4) * 4 + e;
-          const bool ok = key < p && gq >= 0 && Gk[key] == gq && Ak[key] && (fut || key <= q);
-          sc[kt][e] = ok ? s[e] * 0.125f : -INFINITY;
+          const bool ok = kgv[e] == kq && (fut || e <= rel);
+          sc[kt][e] = blocked ? (kgv[e] != -4 ? 0.0f : -INFINITY) : ok ? s[e] * 0.125f : -INFINITY;
           mx = fmaxf(mx, sc[kt][e]);
         }
       }
     }
     mx = rows_max(mx);
-    const bool uniform = mx == -INFINITY;
     float sum = 0.0f;
 #pragma unroll
     for (int kt = 0; kt < MAXKT; ++kt) {
       if (kt < nkt) {
 #pragma unroll
         for (int e = 0; e < 4; ++e) {
-          const int key = kt * 16 + (lane >> 4) * 4 + e;
-          const float ev = uniform ? (key < p ? 1.0f : 0.0f) : __expf(sc[kt][e] - mx);
-          sc[kt][e] = ev;
-          sum += ev;
+          sc[kt][e] = __expf(sc[kt][e] - mx);
+          sum += sc[kt][e];
         }
       }
     }
@@ -216,7 +255,7 @@ __global__ __launch_bounds__(256) void k_time_attn(const AttnDesc d) {
         }
 #pragma unroll
         for (int dt = 0; dt < 4; ++dt) {
-          const _Float16* vrow = Vt + (dt * 16 + (lane & 15)) * LDV + 32 * c + (lane >> 4) * 4;
+          const _Float16* vrow = Vt + (dt * 16 + (lane & 15)) * LDV + 32 * c + part * 4;
           const half4 lo = *reinterpret_cast<const half4*>(vrow);
           const half4 hi = *reinterpret_cast<const half4*>(vrow + 16);
           const half8 bv = {lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
@@ -224,14 +263,13 @@ __global__ __launch_bounds__(256) void k_time_attn(const AttnDesc d) {
         }
       }
     }
-    // Stage O (16 queries x 64 dims) in this tile's Q rows, which only this
-    // wave reads, then write 16-byte row chunks.  LDS operations of one wave
-    // complete in order.
-    _Float16* ost = Qs + qt * 16 * LDH;
+    // Stage O (16 queries x 64 dims) in the wave's own region, then write
+    // 16-byte row chunks.  LDS operations of one wave complete in order; the
+    // fences keep the compiler from moving the reads above the writes.
 #pragma unroll
     for (int e = 0; e < 4; ++e)
 #pragma unroll
-      for (int dt = 0; dt < 4; ++dt) ost[((lane >> 4) * 4 + e) * LDH + dt * 16 + (lane & 15)] = (_Float16)o[dt][e];
+      for (int dt = 0; dt < 4; ++dt) ost[(part * 4 + e) * LDH + dt * 16 + (lane & 15)] = (_Float16)o[dt][e];
     __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
     __builtin_amdgcn_wave_barrier();
     __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
@@ -242,6 +280,10 @@ __global__ __launch_bounds__(256) void k_time_attn(const AttnDesc d) {
       if (qrow_i < p)
         *reinterpret_cast<uint4*>(d.out + (row0 + qrow_i) * E + h * HD + cc) = *reinterpret_cast<const uint4*>(ost + rr * LDH + cc);
     }
+    // the next tile's staging writes must not pass these reads
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
   }
 }
 
@@ -340,24 +382,27 @@ void check_common(const AttnDesc& d) {
 void launch_time_attention(const AttnDesc& d, hipStream_t s) {
   if (d.v <= 0 || d.p <= 0) return;
   check_common(d);
-  if (!d.att || !d.fut || !d.rope_cos || !d.rope_sin || !d.rope_scale || !d.rope_scale_inv)
-    throw Error(T0H_ERR_INVALID_ARG, "time attention: null pointer");
+  if (!d.att || !d.fut || !d.rope_q || !d.rope_k) throw Error(T0H_ERR_INVALID_ARG, "time attention: null pointer");
   if (d.p > T0H_MAX_PATCHES)
     throw Error(T0H_ERR_UNSUPPORTED, "time attention: window of " + std::to_string(d.p) + " patches exceeds " +
                                          std::to_string(T0H_MAX_PATCHES));
+  static_assert(T0H_MAX_PATCHES <= 16 * 16, "the largest instance covers 16 key tiles of 16");
   const size_t lds = time_attn_lds(d.p);
-  const dim3 block(256);
-  if (round_up(d.p, 32) / 16 <= 8) {
-    check_hip(hipFuncSetAttribute(reinterpret_cast<const void*>(&k_time_attn<8>),
-                                  hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds),
+  const int kt = round_up(d.p, 32) / 16;
+  auto go = [&](auto kern) {
+    check_hip(hipFuncSetAttribute(reinterpret_cast<const void*>(kern), hipFuncAttributeMaxDynamicSharedMemorySize,
+                                  (int)lds),
               "hipFuncSetAttribute(k_time_attn)");
-    hipLaunchKernelGGL(k_time_attn<8>, dim3(d.v * d.heads), block, lds, s, d);
-  } else {
-    check_hip(hipFuncSetAttribute(reinterpret_cast<const void*>(&k_time_attn<MAXKT>),
-                                  hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds),
-              "hipFuncSetAttribute(k_time_attn)");
-    hipLaunchKernelGGL(k_time_attn<MAXKT>, dim3(d.v * d.heads), block, lds, s, d);
-  }
+    hipLaunchKernelGGL(kern, dim3(d.v * d.heads), dim3(TA_WAVES * 64), lds, s, d);
+  };
+  if (kt <= 4)
+    go(&k_time_attn<4>);
+  else if (kt <= 8)
+    go(&k_time_attn<8>);
+  else if (kt <= 12)
+    go(&k_time_attn<12>);
+  else
+    go(&k_time_attn<16>);
   check_hip(hipGetLastError(), "k_time_attn launch");
 }
 

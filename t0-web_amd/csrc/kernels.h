@@ -52,12 +52,12 @@ struct AttnDesc {
   const _Float16* qkv = nullptr;  // [v*p, 3E]
   _Float16* out = nullptr;        // [v*p, E]
   int v = 0, p = 0, E = 0, heads = 0;
-  const float* q_norm = nullptr;  // [head_dim]
+  const float* q_norm = nullptr;  // [head_dim] (group layers)
   const float* k_norm = nullptr;
-  const float* rope_cos = nullptr;  // [p, head_dim]
-  const float* rope_sin = nullptr;
-  const float* rope_scale = nullptr;      // xpos scale applied to q
-  const float* rope_scale_inv = nullptr;  // its reciprocal, applied to k (ops.rs:135-139)
+  // time layers: per side [p, 128] = A | B with QK-norm scale, RoPE and xpos folded in:
+  // rotated[e] = x[e] / rms(x) * A[e] + x[e^1] / rms(x) * B[e]  (xpos: scale on q, its recip on k)
+  const float* rope_q = nullptr;
+  const float* rope_k = nullptr;
   const int* grp = nullptr;          // [v*p] patch group id (-1 = all-PAD patch)
   const uint8_t* att = nullptr;      // [v*p] patch attendable
   const uint8_t* fut = nullptr;      // [v] row is FUTURE (bidirectional time attention)

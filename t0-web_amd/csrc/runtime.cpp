@@ -52,6 +52,7 @@ struct Layer {
   bool group = false;
   Mat qkv, o, w0, w2;
   const float *b_qkv, *b_o, *b0, *b2, *norm, *mlp_norm, *q_norm, *k_norm;
+  std::vector<float> q_norm_h, k_norm_h;  // host copies, folded into the time-attention tables
 };
 
 struct Buf {
@@ -354,6 +355,12 @@ void load_model(t0h_model* m, const uint8_t* bytes, size_t len) {
     L.mlp_norm = vec(p + ".norm.scale");
     L.q_norm = vec(p + ".attention_block.attention.q_norm.scale");
     L.k_norm = vec(p + ".attention_block.attention.k_norm.scale");
+    auto host_vec = [&](const std::string& n) {
+      const float* f = reinterpret_cast<const float*>(host.data() + place.at(n).off);
+      return std::vector<float>(f, f + place.at(n).t->n);
+    };
+    L.q_norm_h = host_vec(p + ".attention_block.attention.q_norm.scale");
+    L.k_norm_h = host_vec(p + ".attention_block.attention.k_norm.scale");
     m->quantizable_bytes += L.qkv.bytes + L.o.bytes + L.w0.bytes + L.w2.bytes;
     m->layers.push_back(L);
   }
@@ -410,16 +417,34 @@ void upload_segments(t0h_model* m, const std::vector<int64_t>& row_group, bool c
   put(m, "seg_len", len.data(), v);
 }
 
+// Per layer and side (q, k), one [p, 128] f32 table folding the QK-norm scale,
+// the rotation and the xpos scale (q: scale, k: scale.recip() in f32) of each
+// element, so that rotated = inv_rms * (x[e] * A[e] + x[e^1] * B[e]) with
+//   A[e] = norm[e] * cos[e] * xs[e]             (columns 0..63)
+//   B[e] = -+ norm[e^1] * sin[e] * xs[e]        (columns 64..127; - for even e)
+// which is ops.rs:132-142 applied to ops.rs:175-181's normalized rows, with the
+// f32 table values multiplied in f64 and rounded once.
 void ensure_rope(t0h_model* m, int p) {
   if (m->ws.rope_p == p) return;
-  std::vector<float> a, b, c;
-  rope_tables(p, 64, a, b, c);
-  put(m, "rope_cos", a.data(), a.size());
-  put(m, "rope_sin", b.data(), b.size());
-  put(m, "rope_scale", c.data(), c.size());
-  std::vector<float> ci(c.size());
-  for (size_t i = 0; i < c.size(); ++i) ci[i] = 1.0f / c[i];  // k-side table, scale.recip() in f32
-  put(m, "rope_scale_inv", ci.data(), ci.size());
+  std::vector<float> cs, sn, sc;
+  rope_tables(p, 64, cs, sn, sc);
+  const size_t per = (size_t)p * 128;
+  std::vector<float> t(m->layers.size() * 2 * per, 0.f);
+  for (size_t li = 0; li < m->layers.size(); ++li) {
+    const Layer& L = m->layers[li];
+    for (int side = 0; side < 2; ++side) {
+      const std::vector<float>& nrm = side ? L.k_norm_h : L.q_norm_h;
+      float* dst = t.data() + (li * 2 + side) * per;
+      for (int pos = 0; pos < p; ++pos)
+        for (int e = 0; e < 64; ++e) {
+          const size_t i = (size_t)pos * 64 + e;
+          const double xs = side ? (double)(1.0f / sc[i]) : (double)sc[i];
+          dst[(size_t)pos * 128 + e] = (float)((double)nrm[e] * (double)cs[i] * xs);
+          dst[(size_t)pos * 128 + 64 + e] = (float)((e & 1 ? 1.0 : -1.0) * (double)nrm[e ^ 1] * (double)sn[i] * xs);
+        }
+    }
+  }
+  put(m, "rope", t.data(), t.size());
   m->ws.rope_p = p;
 }
 
@@ -499,10 +524,7 @@ void encode_and_layers(t0h_model* m, int v, int p, const PatchMeta& pm, float* t
   ad.p = p;
   ad.E = E;
   ad.heads = (int)c.num_heads;
-  ad.rope_cos = ws_get<float>(m, "rope_cos", (size_t)p * 64);
-  ad.rope_sin = ws_get<float>(m, "rope_sin", (size_t)p * 64);
-  ad.rope_scale = ws_get<float>(m, "rope_scale", (size_t)p * 64);
-  ad.rope_scale_inv = ws_get<float>(m, "rope_scale_inv", (size_t)p * 64);
+  const float* rope = ws_get<float>(m, "rope", m->layers.size() * 2 * (size_t)p * 128);
   ad.grp = pm.grp;
   ad.att = pm.att;
   ad.fut = pm.fut;
@@ -521,6 +543,8 @@ void encode_and_layers(t0h_model* m, int v, int p, const PatchMeta& pm, float* t
     }
     ad.q_norm = L.q_norm;
     ad.k_norm = L.k_norm;
+    ad.rope_q = rope + li * 2 * (size_t)p * 128;
+    ad.rope_k = ad.rope_q + (size_t)p * 128;
     if (L.group) {
       ProfScope ps_(m, "attn_group");
       launch_group_attention(ad, s);
