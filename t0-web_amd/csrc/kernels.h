@@ -65,6 +65,7 @@ struct AttnDesc {
   const int* perm = nullptr;         // [v]
   const int* seg_begin = nullptr;    // [v]
   const int* seg_len = nullptr;      // [v]
+  int seg_max = 0;                   // longest segment (selects the kernel)
 };
 void launch_time_attention(const AttnDesc& d, hipStream_t s);
 void launch_group_attention(const AttnDesc& d, hipStream_t s);

@@ -74,6 +74,7 @@ struct Workspace {
   std::unordered_map<std::string, Stage> stages;
   uint64_t allocs = 0;
   int rope_p = -1;
+  int seg_max = 0;  // longest group segment of the last upload_segments
 };
 
 // Per-kernel-kind timing with HIP events recorded on the model's stream around
@@ -415,6 +416,7 @@ void upload_segments(t0h_model* m, const std::vector<int64_t>& row_group, bool c
   put(m, "perm", perm.data(), v);
   put(m, "seg_begin", begin.data(), v);
   put(m, "seg_len", len.data(), v);
+  m->ws.seg_max = v ? *std::max_element(len.begin(), len.end()) : 0;
 }
 
 // Per layer and side (q, k), one [p, 128] f32 table folding the QK-norm scale,
@@ -531,6 +533,7 @@ void encode_and_layers(t0h_model* m, int v, int p, const PatchMeta& pm, float* t
   ad.perm = perm;
   ad.seg_begin = seg_begin;
   ad.seg_len = seg_len;
+  ad.seg_max = m->ws.seg_max;
   for (size_t li = 0; li < m->layers.size(); ++li) {
     const Layer& L = m->layers[li];
     {
