@@ -1142,6 +1142,44 @@ __device__ __forceinline__ float wave_reduce_scatter(float (&v)[V], int lane, in
   return v[0];
 }
 
+// Output stage shared by the small-M kernels: fin[r * MT + mt] holds the dot
+// product of weight row r of the workgroup's segment (SwiGLU: gate rows, then
+// the up rows at + V/2) with activation row m0 + mt; bias and epilogue applied.
+template <int EPI, int MT, int NR>
+__device__ __forceinline__ void gemv_store(const GemmDesc& d, const float* fin, int tid, int r0, int valid, int m0) {
+  constexpr int V = NR * MT;
+  const int M = d.M, N = d.N;
+  if (EPI == EPI_SWIGLU_F16) {
+    if (tid < V / 2) {
+      const int r = tid / MT, mt = tid % MT;
+      const int g = r0 + r, m = m0 + mt;
+      if (r < valid && m < M) {
+        const float gate = fin[tid] + (d.bias ? d.bias[g] : 0.0f);
+        const float up = fin[tid + V / 2] + (d.bias ? d.bias[N + g] : 0.0f);
+        static_cast<_Float16*>(d.y)[(size_t)m * d.ldy + g] = (_Float16)(silu(gate) * up);
+      }
+    }
+  } else if (tid < V) {
+    const int r = tid / MT, mt = tid % MT;
+    const int n = r0 + r, m = m0 + mt;
+    if (r < valid && m < M) {
+      float v = fin[tid] + (d.bias ? d.bias[n] : 0.0f);
+      const size_t o = (size_t)m * d.ldy + n;
+      if (EPI == EPI_RESID_F32) {
+        float* y = static_cast<float*>(d.y);
+        y[o] = y[o] + v;
+      } else {
+        if (EPI == EPI_STORE_F32 && d.row_add) v = v + d.row_add[(size_t)d.row_add_idx[m] * N + n];
+        if (d.relu) v = v > 0.0f ? v : 0.0f;
+        if (EPI == EPI_STORE_F32)
+          static_cast<float*>(d.y)[o] = v;
+        else
+          static_cast<_Float16*>(d.y)[o] = (_Float16)v;
+      }
+    }
+  }
+}
+
 template <int WT, bool A32, int EPI, int MT>
 __global__ __launch_bounds__(256) void k_gemv(const GemmDesc d) {
   extern __shared__ __align__(16) uint8_t sm[];
@@ -1214,35 +1252,122 @@ __global__ __launch_bounds__(256) void k_gemv(const GemmDesc d) {
   float* fin = red + 4 * V;
   if (tid < V) fin[tid] = red[tid] + red[V + tid] + red[2 * V + tid] + red[3 * V + tid];
   __syncthreads();
-  if (EPI == EPI_SWIGLU_F16) {
-    if (tid < V / 2) {
-      const int r = tid / MT, mt = tid % MT;
-      const int g = r0 + r, m = m0 + mt;
-      if (r < valid && m < M) {
-        const float gate = fin[tid] + (d.bias ? d.bias[g] : 0.0f);
-        const float up = fin[tid + V / 2] + (d.bias ? d.bias[N + g] : 0.0f);
-        static_cast<_Float16*>(d.y)[(size_t)m * d.ldy + g] = (_Float16)(silu(gate) * up);
-      }
+  gemv_store<EPI, MT, GV_NR>(d, fin, tid, r0, valid, m0);
+}
+
+// ---------------------------------------------------------------------------
+// Small-M kernel for Q8_0 / Q4_0 weights with K % 64 == 0 (M <= MT <= 16).
+// 16 lanes per weight row, 16 rows per workgroup (SwiGLU: 8 gate rows and
+// their 8 up rows).  A lane owns whole 2-block spans of its row (68 B Q8_0 /
+// 36 B Q4_0; a row is K/64 spans, so every span is 4-byte aligned), all of
+// them loaded before the first is used.  Dequantization is exact f32: with u
+// the offset byte (q + 128) or the nibble (q + 8), fma(d, u, -128 d) and
+// fma(d, u, -8 d) are the exact product f32(d) * q (gguf.rs:116-126, 159-174).
+// Activations of the MT rows are staged per 1024-wide K tile in LDS as f32
+// with each 64-value span padded to 68 floats, so the 16 spans a row group
+// reads in one instruction fall in distinct banks (the four row groups of a
+// wave read the same addresses: broadcast).  f32 FMAs, then a 16-lane DPP
+// reduction and the shared output stage.
+// ---------------------------------------------------------------------------
+constexpr int GS_NR = 16, GS_TILE = 1024, GS_XS = (GS_TILE / 64) * 68;
+
+template <int WT, bool A32, int EPI, int MT, int NP>
+__global__ __launch_bounds__(256) void k_gemv_s(const GemmDesc d) {
+  extern __shared__ __align__(16) float xs[];
+  constexpr int DW = WT == T0H_Q8_0 ? 17 : 9;  // dwords per 2-block span
+  constexpr bool SWI = EPI == EPI_SWIGLU_F16;
+  const int tid = threadIdx.x, g = tid >> 4, sp = tid & 15;
+  const int M = d.M, N = d.N, K = d.K, nsp = K / 64;
+  const int r0 = blockIdx.x * (SWI ? GS_NR / 2 : GS_NR);
+  const int valid = min(SWI ? GS_NR / 2 : GS_NR, N - r0);
+  const int rloc = SWI ? (g & 7) : g;
+  // rows past N read row r0 (never stored)
+  const int wrow = (rloc < valid ? r0 + rloc : r0) + (SWI && g >= 8 ? N : 0);
+  const uint32_t* wr = reinterpret_cast<const uint32_t*>(d.w) + (size_t)wrow * nsp * DW;
+  uint32_t w[NP][DW];
+#pragma unroll
+  for (int t = 0; t < NP; ++t) {
+    const int s = t * 16 + sp;
+    if (s < nsp) {
+      const uint32_t* src = wr + s * DW;  // DW contiguous dwords
+#pragma unroll
+      for (int i = 0; i < DW; ++i) w[t][i] = src[i];
     }
-  } else if (tid < V) {
-    const int r = tid / MT, mt = tid % MT;
-    const int n = r0 + r, m = m0 + mt;
-    if (r < valid && m < M) {
-      float v = fin[tid] + (d.bias ? d.bias[n] : 0.0f);
-      const size_t o = (size_t)m * d.ldy + n;
-      if (EPI == EPI_RESID_F32) {
-        float* y = static_cast<float*>(d.y);
-        y[o] = y[o] + v;
-      } else {
-        if (EPI == EPI_STORE_F32 && d.row_add) v = v + d.row_add[(size_t)d.row_add_idx[m] * N + n];
-        if (d.relu) v = v > 0.0f ? v : 0.0f;
-        if (EPI == EPI_STORE_F32)
-          static_cast<float*>(d.y)[o] = v;
-        else
-          static_cast<_Float16*>(d.y)[o] = (_Float16)v;
+  }
+  float acc[MT];
+#pragma unroll
+  for (int m = 0; m < MT; ++m) acc[m] = 0.0f;
+
+#pragma unroll
+  for (int t = 0; t < NP; ++t) {
+    const int k0 = t * GS_TILE;
+    if (k0 >= K) break;
+    const int kn = min(GS_TILE, K - k0);
+    if (t) __syncthreads();  // the previous tile is consumed
+    for (int i = tid; i < MT * (kn / 4); i += 256) {
+      const int m = i / (kn / 4), k4 = (i % (kn / 4)) * 4;
+      float4 v = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+      if (m < M) {
+        if (A32) {
+          v = *reinterpret_cast<const float4*>(static_cast<const float*>(d.a) + (size_t)m * d.lda + k0 + k4);
+        } else {
+          const half4 h = *reinterpret_cast<const half4*>(static_cast<const _Float16*>(d.a) + (size_t)m * d.lda + k0 + k4);
+          v = make_float4((float)h[0], (float)h[1], (float)h[2], (float)h[3]);
+        }
+      }
+      *reinterpret_cast<float4*>(xs + m * GS_XS + (k4 >> 6) * 68 + (k4 & 63)) = v;
+    }
+    __syncthreads();
+    const int s = t * 16 + sp;
+    if (s < nsp) {
+      const uint32_t* r = w[t];
+      const float* xr = xs + sp * 68;
+#pragma unroll
+      for (int h = 0; h < 2; ++h) {
+        // block h of the span: d at byte (DW*2)*h, quants after it
+        const int bo = h * (DW * 2);  // byte offset of the block (34 or 18 per block)
+        const uint32_t dw = r[bo >> 2];
+        const float dv = (float)__builtin_bit_cast(_Float16, (uint16_t)((bo & 3) ? (dw >> 16) : (dw & 0xffff)));
+        const float nofs = (WT == T0H_Q8_0 ? -128.0f : -8.0f) * dv;
+#pragma unroll
+        for (int pc = 0; pc < 4; ++pc) {  // 8 consecutive values k = 32h + 8pc .. +7
+          float wv[8];
+#pragma unroll
+          for (int e = 0; e < 8; ++e) {
+            uint32_t u;
+            if (WT == T0H_Q8_0) {
+              const int b = bo + 2 + pc * 8 + e;  // byte of value 8pc + e
+              u = ((r[b >> 2] >> (8 * (b & 3))) & 0xffu) ^ 0x80u;
+            } else {
+              const int j = (pc & 1) * 8 + e;  // quant byte; high nibbles for values >= 16
+              const int b = bo + 2 + j;
+              u = (r[b >> 2] >> (8 * (b & 3) + (pc >= 2 ? 4 : 0))) & 0xfu;
+            }
+            wv[e] = fmaf(dv, (float)u, nofs);
+          }
+#pragma unroll
+          for (int m = 0; m < MT; ++m) {
+            const float4 xa = *reinterpret_cast<const float4*>(xr + m * GS_XS + 32 * h + 8 * pc);
+            const float4 xb = *reinterpret_cast<const float4*>(xr + m * GS_XS + 32 * h + 8 * pc + 4);
+            float a = acc[m];
+            a = fmaf(wv[0], xa.x, a); a = fmaf(wv[1], xa.y, a); a = fmaf(wv[2], xa.z, a); a = fmaf(wv[3], xa.w, a);
+            a = fmaf(wv[4], xb.x, a); a = fmaf(wv[5], xb.y, a); a = fmaf(wv[6], xb.z, a); a = fmaf(wv[7], xb.w, a);
+            acc[m] = a;
+          }
+        }
       }
     }
   }
+#pragma unroll
+  for (int m = 0; m < MT; ++m) acc[m] = lane_sum16(acc[m]);
+  __syncthreads();  // activations no longer needed: reuse LDS for the row sums
+  float* fin = xs;
+  if (sp == 0) {
+#pragma unroll
+    for (int m = 0; m < MT; ++m) fin[g * MT + m] = acc[m];
+  }
+  __syncthreads();
+  gemv_store<EPI, MT, GS_NR>(d, fin, tid, r0, valid, 0);
 }
 
 // ---------------------------------------------------------------------------
@@ -1376,8 +1501,36 @@ void run_gemv(const GemmDesc& d, hipStream_t s) {
   check_hip(hipGetLastError(), "k_gemv launch");
 }
 
+template <int WT, bool A32, int EPI, int MT, int NP>
+void run_gemv_s(const GemmDesc& d, hipStream_t s) {
+  const size_t lds = (size_t)MT * GS_XS * sizeof(float);
+  const int per = EPI == EPI_SWIGLU_F16 ? GS_NR / 2 : GS_NR;
+  check_hip(hipFuncSetAttribute(reinterpret_cast<const void*>(&k_gemv_s<WT, A32, EPI, MT, NP>),
+                                hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds),
+            "hipFuncSetAttribute(k_gemv_s)");
+  hipLaunchKernelGGL((k_gemv_s<WT, A32, EPI, MT, NP>), dim3((d.N + per - 1) / per), dim3(256), lds, s, d);
+  check_hip(hipGetLastError(), "k_gemv_s launch");
+}
+
+template <int WT, bool A32, int EPI, int MT>
+void dispatch_gemv_s(const GemmDesc& d, hipStream_t s) {
+  if (d.K <= GS_TILE)
+    run_gemv_s<WT, A32, EPI, MT, 1>(d, s);
+  else if (d.K <= 2 * GS_TILE)
+    run_gemv_s<WT, A32, EPI, MT, 2>(d, s);
+  else
+    run_gemv_s<WT, A32, EPI, MT, 4>(d, s);
+}
+
 template <int WT, bool A32, int EPI>
 void dispatch_gemv(const GemmDesc& d, hipStream_t s) {
+  if constexpr (WT != T0H_F16) {
+    if (d.M <= 16 && d.K % 64 == 0 && d.K <= 4 * GS_TILE) {
+      if (d.M == 1) return dispatch_gemv_s<WT, A32, EPI, 1>(d, s);
+      if (d.M <= 4) return dispatch_gemv_s<WT, A32, EPI, 4>(d, s);
+      return dispatch_gemv_s<WT, A32, EPI, 16>(d, s);
+    }
+  }
   if (d.M == 1)
     run_gemv<WT, A32, EPI, 1>(d, s);
   else if (d.M == 2)

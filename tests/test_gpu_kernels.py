@@ -200,3 +200,31 @@ def test_register_b_gemm_edges(torch_cuda, t0hip, oracle, rng, qtype, tile, epi,
     if epi == 3:
         n -= n % 8
     check_forward_gemm(torch_cuda, t0hip, oracle, rng, qtype, tile, epi, m, k, n, sample=False)
+
+
+@pytest.mark.parametrize("qtype", [8, 2])
+@pytest.mark.parametrize("m,k,n", [(1, 2560, 200), (4, 4096, 72), (16, 768, 40), (7, 2048, 17), (16, 1088, 24)])
+def test_small_m_kernel(torch_cuda, t0hip, oracle, rng, qtype, m, k, n):
+    """The small-M kernel (M <= 16, K % 64 == 0, K <= 4096) through t0h_gemm_q:
+    exact f32 dequantization and accumulation, so the 1e-5 gate of the
+    reference's f32 kernels holds; a partial last K tile (K = 2560, 1088), N not
+    a multiple of the 16 weight rows of a workgroup."""
+    W = (0.02 * rng.standard_normal((n, k))).astype(np.float32)
+    x = rng.standard_normal((m, k)).astype(np.float32)
+    b = (0.02 * rng.standard_normal(n)).astype(np.float32)
+    blocks = oracle.quantize(qtype, W)
+    deq = oracle.dequantize(qtype, blocks, n * k).reshape(n, k).astype(np.float64)
+    want = x.astype(np.float64) @ deq.T + b
+    got = run_gemm(torch_cuda, t0hip, qtype, blocks, x, b, n)
+    assert rel_err(got, want) < 1e-5, (m, k, n)
+    got = run_gemm(torch_cuda, t0hip, qtype, blocks, x, b, n, act=1)
+    assert rel_err(got, np.maximum(want, 0.0)) < 1e-5, (m, k, n)
+
+
+@pytest.mark.parametrize("qtype", [8, 2])
+@pytest.mark.parametrize("epi", [0, 1, 2, 3])
+@pytest.mark.parametrize("m,k,n", [(1, 768, 136), (9, 2048, 72), (16, 768, 40)])
+def test_small_m_forward_epilogues(torch_cuda, t0hip, oracle, rng, qtype, epi, m, k, n):
+    """The forward's GEMMs at M <= 16 (a single series): f16 activations, epilogues
+    bias / f16 store / residual add / SwiGLU on the small-M kernel."""
+    check_forward_gemm(torch_cuda, t0hip, oracle, rng, qtype, 0, epi, m, k, n, sample=False)
