@@ -1256,6 +1256,144 @@ __global__ __launch_bounds__(256) void k_gemv(const GemmDesc d) {
 }
 
 // ---------------------------------------------------------------------------
+// Medium-M kernel (16 < M < 1024, Q8_0 / Q4_0, K % 64 == 0).  A workgroup owns
+// a 32*TI-row x 32-column output tile (SwiGLU: 16 hidden units in the PAIR
+// layout of k_gemm_bf) and splits K over its waves, KR 64-wide steps each.  A
+// wave issues every load of its K range before the first MFMA: its weight
+// row's blocks in the k_gemm_bf lane layout (lane l holds block l/32 of each
+// step's 2-block span of row l%32, slice c taking k = 32(l/32) + 8c .. +7) and
+// its activation fragments straight from global memory (f32 converted to
+// f16), then runs 4*KR*TI MFMAs.  The partial tiles meet in LDS; wave i sums
+// 32-row slice i and runs the shared staged epilogue on it.  These shapes are
+// latency-bound: one load round trip, a short MFMA chain and one reduction
+// replace a K loop per workgroup.
+// ---------------------------------------------------------------------------
+// B fragment of slice c from a lane's raw dwords of one step (the dequant of
+// k_gemm_bf in one piece): exact small integers through the 0x6400 exponent
+// trick, the offset removed and d applied in packed f16 (one rounding of d*q).
+template <int WT>
+__device__ __forceinline__ half8 dq_frag(const uint32_t* r, int c, int h) {
+  const uint32_t qsel = h ? 0x07060504u : 0x05040302u;
+  const uint32_t dsel = h ? 0x03020302u : 0x01000100u;
+  const int i = WT == T0H_Q8_0 ? 2 * c : 2 * (c & 1);
+  uint32_t qa = perm(r[i + 1], r[i], qsel), qb = perm(r[i + 2], r[i + 1], qsel);
+  if (WT == T0H_Q4_0) {
+    if (c >= 2) {
+      qa >>= 4;
+      qb >>= 4;
+    }
+    qa &= 0x0f0f0f0fu;
+    qb &= 0x0f0f0f0fu;
+  } else {
+    qa ^= 0x80808080u;
+    qb ^= 0x80808080u;
+  }
+  const half2v dd = __builtin_bit_cast(half2v, perm(r[0], r[0], dsel));
+  const uint32_t t[4] = {perm(0x64646464u, qa, 0x04010400u), perm(0x64646464u, qa, 0x04030402u),
+                         perm(0x64646464u, qb, 0x04010400u), perm(0x64646464u, qb, 0x04030402u)};
+  const _Float16 o = (_Float16)(WT == T0H_Q8_0 ? 1152.0f : 1032.0f);
+  const half2v off = {o, o};
+  uint32_t v[4];
+#pragma unroll
+  for (int e = 0; e < 4; ++e) v[e] = __builtin_bit_cast(uint32_t, (__builtin_bit_cast(half2v, t[e]) - off) * dd);
+  return __builtin_bit_cast(half8, make_uint4(v[0], v[1], v[2], v[3]));
+}
+
+template <int WT, bool A32, int EPI, int TI, int KR>
+__global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2))) void k_gemm_mid(const GemmDesc d) {
+  constexpr bool SWI = EPI == EPI_SWIGLU_F16;
+  constexpr int NWD = WT == T0H_Q8_0 ? 9 : 5, SWD = WT == T0H_Q8_0 ? 17 : 9;
+  constexpr int W = SWI ? 16 : 32;  // output columns per tile
+  extern __shared__ __align__(16) float red[];
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6, nw = blockDim.x >> 6;
+  const int h = lane >> 5, lc = lane & 31;
+  const int M = d.M, N = d.N, K = d.K, KT = K / 64;
+  const int strips = (N + W - 1) / W;
+  const int tn = blockIdx.x % strips, m0 = (blockIdx.x / strips) * (32 * TI);
+  int wrow;
+  bool ok;
+  if (SWI) {
+    const int g = tn * 16 + (lc & 15);
+    ok = g < N;
+    wrow = lc < 16 ? g : N + g;
+  } else {
+    wrow = tn * 32 + lc;
+    ok = wrow < N;
+  }
+  // rows past N read row 0, activation rows past M read row M-1 (never stored)
+  const uint32_t* wsrc =
+      static_cast<const uint32_t*>(d.w) + (size_t)(ok ? wrow : 0) * ((K / 32) * block_bytes(WT) / 4) + h * (NWD - 1);
+  const int s0 = wave * KR;
+  uint32_t wr[KR][NWD];
+#pragma unroll
+  for (int s = 0; s < KR; ++s)
+    if (s0 + s < KT) {
+      const uint32_t* src = wsrc + (s0 + s) * SWD;  // NWD contiguous dwords
+#pragma unroll
+      for (int i = 0; i < NWD; ++i) wr[s][i] = src[i];
+    }
+  half8 af[KR][4][TI];
+#pragma unroll
+  for (int i = 0; i < TI; ++i) {
+    const size_t row = (size_t)min(m0 + 32 * i + lc, M - 1) * d.lda;
+#pragma unroll
+    for (int s = 0; s < KR; ++s)
+      if (s0 + s < KT) {
+#pragma unroll
+        for (int c = 0; c < 4; ++c) {
+          const size_t k = (size_t)(s0 + s) * 64 + 32 * h + 8 * c;
+          if (A32) {
+            const float4* src = reinterpret_cast<const float4*>(static_cast<const float*>(d.a) + row + k);
+            const float4 x0 = src[0], x1 = src[1];
+            af[s][c][i] = (half8){(_Float16)x0.x, (_Float16)x0.y, (_Float16)x0.z, (_Float16)x0.w,
+                                  (_Float16)x1.x, (_Float16)x1.y, (_Float16)x1.z, (_Float16)x1.w};
+          } else {
+            af[s][c][i] = *reinterpret_cast<const half8*>(static_cast<const _Float16*>(d.a) + row + k);
+          }
+        }
+      }
+  }
+  floatx16 acc[TI][1];
+#pragma unroll
+  for (int i = 0; i < TI; ++i)
+#pragma unroll
+    for (int e = 0; e < 16; ++e) acc[i][0][e] = 0.0f;
+#pragma unroll
+  for (int s = 0; s < KR; ++s)
+    if (s0 + s < KT) {
+#pragma unroll
+      for (int c = 0; c < 4; ++c) {
+        const half8 b = dq_frag<WT>(wr[s], c, h);
+#pragma unroll
+        for (int i = 0; i < TI; ++i) acc[i][0] = __builtin_amdgcn_mfma_f32_32x32x16_f16(af[s][c][i], b, acc[i][0], 0, 0, 0);
+      }
+    }
+  // partial tiles: [wave][slice][quad][lane] float4s (lane-contiguous, no bank conflicts)
+#pragma unroll
+  for (int i = 0; i < TI; ++i)
+#pragma unroll
+    for (int q = 0; q < 4; ++q)
+      reinterpret_cast<float4*>(red)[((wave * TI + i) * 4 + q) * 64 + lane] =
+          make_float4(acc[i][0][4 * q], acc[i][0][4 * q + 1], acc[i][0][4 * q + 2], acc[i][0][4 * q + 3]);
+  __syncthreads();
+  if (wave >= TI) return;
+  floatx16 sum[1][1];
+#pragma unroll
+  for (int e = 0; e < 16; ++e) sum[0][0][e] = 0.0f;
+  for (int w = 0; w < nw; ++w)
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+      const float4 v = reinterpret_cast<const float4*>(red)[((w * TI + wave) * 4 + q) * 64 + lane];
+      sum[0][0][4 * q] += v.x;
+      sum[0][0][4 * q + 1] += v.y;
+      sum[0][0][4 * q + 2] += v.z;
+      sum[0][0][4 * q + 3] += v.w;
+    }
+  // staging after the partials (other slices may still be reading them)
+  store_tile<EPI, 1, 1>(d, sum, red + nw * TI * 16 * 64, wave, lane, m0 + 32 * wave, tn * W);
+}
+
+// ---------------------------------------------------------------------------
 // Small-M kernel for Q8_0 / Q4_0 weights with K % 64 == 0 (M <= MT <= 16).
 // 16 lanes per weight row, 16 rows per workgroup (SwiGLU: 8 gate rows and
 // their 8 up rows).  A lane owns whole 2-block spans of its row (68 B Q8_0 /
@@ -1270,6 +1408,12 @@ __global__ __launch_bounds__(256) void k_gemv(const GemmDesc d) {
 // reduction and the shared output stage.
 // ---------------------------------------------------------------------------
 constexpr int GS_NR = 16, GS_TILE = 1024, GS_XS = (GS_TILE / 64) * 68;
+// The medium-M kernel takes 16 < M < 1024 up to MID_MN_MAX outputs: each of its
+// 32-column workgroups reads the whole activation block, so past about 512 x
+// 2304 outputs the LDS-staged 128x128 tiles measured faster (M = 512, N = 4096:
+// 25 vs 32 us; N = 2304: 24 vs 22 us).
+constexpr int MID_M_MAX = 1024;
+constexpr long long MID_MN_MAX = 512LL * 2304;
 
 template <int WT, bool A32, int EPI, int MT, int NP>
 __global__ __launch_bounds__(256) void k_gemv_s(const GemmDesc d) {
@@ -1539,9 +1683,50 @@ void dispatch_gemv(const GemmDesc& d, hipStream_t s) {
     run_gemv<WT, A32, EPI, 4>(d, s);
 }
 
+// Waves of KR steps over K (at most 8 per workgroup, two per SIMD, so a wave
+// may hold its KR steps of operands: up to 256 registers); lds: the partial
+// tiles and the epilogue staging of TI waves.
+template <int WT, bool A32, int EPI, int TI, int KR>
+void run_gemm_mid(const GemmDesc& d, hipStream_t s) {
+  // at least one wave per 32-row slice: slice i is summed and stored by wave i
+  const int KT = d.K / 64, nw = std::max(TI, (KT + KR - 1) / KR);
+  if (nw > 8) throw Error(T0H_ERR_UNSUPPORTED, "gemm: K too large for the medium-M kernel");
+  const int W = EPI == EPI_SWIGLU_F16 ? 16 : 32;
+  const size_t lds = (size_t)nw * TI * 16 * 64 * 4 + (size_t)TI * 32 * (W + 4) * 4;
+  const int strips = (d.N + W - 1) / W, mt = (d.M + 32 * TI - 1) / (32 * TI);
+  check_hip(hipFuncSetAttribute(reinterpret_cast<const void*>(&k_gemm_mid<WT, A32, EPI, TI, KR>),
+                                hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds),
+            "hipFuncSetAttribute(k_gemm_mid)");
+  hipLaunchKernelGGL((k_gemm_mid<WT, A32, EPI, TI, KR>), dim3(strips * mt), dim3(64 * nw), lds, s, d);
+  check_hip(hipGetLastError(), "k_gemm_mid launch");
+}
+
+// Shapes the medium-M kernel takes: K % 64 == 0 and K <= 4096 (f16 activations)
+// or 2048 (f32); 32-row tiles for f32 activations or M <= 32, else 64.
+bool mid_ok(const GemmDesc& d) { return d.K % 64 == 0 && d.K <= (d.a_f32 ? 2048 : 4096); }
+
+template <int WT, bool A32, int EPI>
+void dispatch_mid(const GemmDesc& d, hipStream_t s) {
+  const int KT = d.K / 64;
+  if (A32 || d.M <= 32 || KT > 32) {
+    if (KT <= 16) return run_gemm_mid<WT, A32, EPI, 1, 2>(d, s);
+    if (KT <= 32) return run_gemm_mid<WT, A32, EPI, 1, 4>(d, s);
+    if constexpr (!A32) return run_gemm_mid<WT, A32, EPI, 1, 8>(d, s);
+  } else {
+    if (KT <= 16) return run_gemm_mid<WT, A32, EPI, 2, 2>(d, s);
+    return run_gemm_mid<WT, A32, EPI, 2, 4>(d, s);
+  }
+  throw Error(T0H_ERR_UNSUPPORTED, "gemm: shape outside the medium-M kernel");
+}
+
 template <int WT, bool A32, int EPI>
 void dispatch_w(const GemmDesc& d, int force, hipStream_t s) {
-  const bool mfma = force == 1 || force >= 3 || (force == 0 && d.M > 16);
+  if constexpr (WT != T0H_F16) {
+    // medium M (force 0) or force 9
+    const bool mid = force == 0 && d.M > 16 && d.M < MID_M_MAX && (long long)d.M * d.N <= MID_MN_MAX;
+    if ((force == 9 || mid) && mid_ok(d)) return dispatch_mid<WT, A32, EPI>(d, s);
+  }
+  const bool mfma = force == 1 || (force >= 3 && force != 9) || (force == 0 && d.M > 16);
   if (mfma) {
     const int tile = force >= 3 ? force - 2 : 0;
     if (d.K % 64 == 0)

@@ -35,10 +35,12 @@ struct GemmDesc {
 };
 
 void launch_gemm(const GemmDesc& d, hipStream_t s);
-// force = 0: pick by M; 1: MFMA tile kernel (tile by shape); 2: bandwidth-bound small-M
-// kernel; 3 / 4 / 5: MFMA kernel with 128x128 / 256x128 / 256x256 tiles; 6: 256x256
-// DMA-fed kernel; 7: 256x256 kernel with register-dequantized weight fragments
-// (6 and 7: K % 64 == 0, f16 activations, quantized weights).
+// force = 0: pick by shape (M <= 16 small-M kernels; 16 < M < 1024 the split-K
+// medium-M kernel up to 512 x 2304 outputs; else MFMA tiles); 1: MFMA tile kernel (tile
+// by shape); 2: small-M kernels; 3 / 4 / 5: MFMA kernel with 128x128 / 256x128 / 256x256
+// tiles; 6: 256x256 DMA-fed kernel; 7 / 8: 256x256 / 256x128 kernels with
+// register-dequantized weight fragments (6-8: K % 64 == 0, f16 activations, quantized
+// weights); 9: medium-M kernel (K % 64 == 0, quantized weights).
 void launch_gemm_forced(const GemmDesc& d, int force, hipStream_t s);
 void launch_dequant(int type, const void* w, size_t n, float* out, hipStream_t s);
 
