@@ -30,6 +30,7 @@
 
 #include <algorithm>
 #include <string>
+#include <type_traits>
 
 #include "kernels.h"
 #include "lanes.h"
@@ -878,7 +879,18 @@ struct BfCfg {
   static constexpr int BN = 32 * NWV, NBUF = NWV == 8 ? 3 : 2, LDS = NBUF * BF_ABUF * 2;
 };
 
-template <int WT, int EPI, int NWV>
+typedef uint32_t u32x8 __attribute__((ext_vector_type(8)));
+// An activation chunk as f16 for the LDS tile: f16 chunks as they are, f32
+// chunks (8 values) rounded to f16.
+__device__ __forceinline__ u32x4 a_f16(u32x4 r) { return r; }
+__device__ __forceinline__ u32x4 a_f16(u32x8 r) {
+  half8 h;
+#pragma unroll
+  for (int e = 0; e < 8; ++e) h[e] = (_Float16)__uint_as_float(r[e]);
+  return __builtin_bit_cast(u32x4, h);
+}
+
+template <int WT, int EPI, int NWV, bool A32>
 __global__ __launch_bounds__(64 * NWV) __attribute__((amdgpu_waves_per_eu(2, 2))) void k_gemm_bf(const GemmDesc d) {
   using C = BfCfg<NWV>;
   constexpr int BN = C::BN, NBUF = C::NBUF;
@@ -911,10 +923,14 @@ __global__ __launch_bounds__(64 * NWV) __attribute__((amdgpu_waves_per_eu(2, 2))
   // row (rows past N read row 0) as a dword offset, plus the dwords
   // (h ? NWD-1 : 0) of each step's 2-block span.
   const int arow = tid >> 3, achunk = tid & 7;
-  const char* const a_tile = static_cast<const char*>(d.a) + (size_t)m0 * d.lda * 2;
+  // f32 activations (A32): a chunk is the 32 bytes of the same 8 values, held raw
+  // until its LDS store converts it to f16
+  constexpr int AB = A32 ? 4 : 2;  // bytes per activation value
+  using AR = std::conditional_t<A32, u32x8, u32x4>;
+  const char* const a_tile = static_cast<const char*>(d.a) + (size_t)m0 * d.lda * AB;
   int aoff[ACH];
 #pragma unroll
-  for (int q = 0; q < ACH; ++q) aoff[q] = (min(m0 + arow + AQS * q, M - 1) - m0) * d.lda * 2 + achunk * 16;
+  for (int q = 0; q < ACH; ++q) aoff[q] = (min(m0 + arow + AQS * q, M - 1) - m0) * d.lda * AB + achunk * 8 * AB;
   int woff;
   {
     int wrow;
@@ -935,7 +951,7 @@ __global__ __launch_bounds__(64 * NWV) __attribute__((amdgpu_waves_per_eu(2, 2))
   const uint32_t qsel = h ? 0x07060504u : 0x05040302u;
   const uint32_t dsel = h ? 0x03020302u : 0x01000100u;
 
-  auto load_a = [&](u32x4& r, int kt, int q) { r = *reinterpret_cast<const u32x4*>(a_tile + kt * (TK * 2) + aoff[q]); };
+  auto load_a = [&](AR& r, int kt, int q) { r = *reinterpret_cast<const AR*>(a_tile + kt * (TK * AB) + aoff[q]); };
   auto a_dst = [&](int buf, int q) {
     return reinterpret_cast<u32x4*>(smem + buf * BF_ABUF + (arow + AQS * q) * LDK + achunk * 8);
   };
@@ -998,7 +1014,7 @@ __global__ __launch_bounds__(64 * NWV) __attribute__((amdgpu_waves_per_eu(2, 2))
     for (int e = 0; e < 16; ++e) acc[i][0][e] = 0.0f;
   uint32_t wr0[NWD], wr1[NWD];
   half8 ring[RING], bf[2];
-  u32x4 ar[ACH];
+  AR ar[ACH];
 
   int abuf = 0;
   // One step: slice c, MFMA i (m = c*TI + i): the ring read of fragment
@@ -1036,7 +1052,7 @@ __global__ __launch_bounds__(64 * NWV) __attribute__((amdgpu_waves_per_eu(2, 2))
           else
             dq(nxt, 0, i >> 1, bf[n]);
         }
-        if (c == 3 && i < ACH) *a_dst(NBUF == 3 ? b2 : b1, i) = ar[i];
+        if (c == 3 && i < ACH) *a_dst(NBUF == 3 ? b2 : b1, i) = a_f16(ar[i]);
         __builtin_amdgcn_sched_barrier(0);
       }
     }
@@ -1047,7 +1063,7 @@ __global__ __launch_bounds__(64 * NWV) __attribute__((amdgpu_waves_per_eu(2, 2))
   // Prologue: A(0) (and, with three buffers, A(1)) into the first buffers,
   // W(0), the first ring fragments and the slice-0 B fragment.
   {
-    u32x4 ar1[ACH];
+    AR ar1[ACH];
 #pragma unroll
     for (int q = 0; q < ACH; ++q) load_a(ar[q], 0, q);
     if constexpr (NBUF == 3) {
@@ -1056,10 +1072,10 @@ __global__ __launch_bounds__(64 * NWV) __attribute__((amdgpu_waves_per_eu(2, 2))
     }
     load_b(wr0, 0);
 #pragma unroll
-    for (int q = 0; q < ACH; ++q) *a_dst(0, q) = ar[q];
+    for (int q = 0; q < ACH; ++q) *a_dst(0, q) = a_f16(ar[q]);
     if constexpr (NBUF == 3) {
 #pragma unroll
-      for (int q = 0; q < ACH; ++q) *a_dst(1, q) = ar1[q];
+      for (int q = 0; q < ACH; ++q) *a_dst(1, q) = a_f16(ar1[q]);
     }
   }
   __syncthreads();
@@ -1591,19 +1607,19 @@ void run_gemm_dma(const GemmDesc& d, hipStream_t s) {
   check_hip(hipGetLastError(), "k_gemm_dma launch");
 }
 
-template <int WT, int EPI, int NWV>
+template <int WT, int EPI, int NWV, bool A32 = false>
 void run_gemm_bf(const GemmDesc& d, hipStream_t s) {
   using C = BfCfg<NWV>;
   const int hb = EPI == EPI_SWIGLU_F16 ? C::BN / 2 : C::BN;
   const int n_tiles = ((d.N + hb - 1) / hb) * ((d.M + BF_BM - 1) / BF_BM);
   static bool attr_set = false;  // per instantiation
   if (!attr_set) {
-    check_hip(hipFuncSetAttribute(reinterpret_cast<const void*>(&k_gemm_bf<WT, EPI, NWV>),
+    check_hip(hipFuncSetAttribute(reinterpret_cast<const void*>(&k_gemm_bf<WT, EPI, NWV, A32>),
                                   hipFuncAttributeMaxDynamicSharedMemorySize, C::LDS),
               "hipFuncSetAttribute(k_gemm_bf)");
     attr_set = true;
   }
-  hipLaunchKernelGGL((k_gemm_bf<WT, EPI, NWV>), dim3(n_tiles), dim3(64 * NWV), C::LDS, s, d);
+  hipLaunchKernelGGL((k_gemm_bf<WT, EPI, NWV, A32>), dim3(n_tiles), dim3(64 * NWV), C::LDS, s, d);
   check_hip(hipGetLastError(), "k_gemm_bf launch");
 }
 
@@ -1618,6 +1634,10 @@ void run_gemm_tiled(const GemmDesc& d, int tile, hipStream_t s) {
     tile = 1;
     if constexpr (!A32 && K64 && WT != T0H_F16)
       if (d.M >= 1024) tile = EPI != EPI_SWIGLU_F16 && d.N >= 1536 ? 5 : 6;
+    // f32 activations (f32 stores only): the 256x256 register-operand kernel
+    // converts them while staging
+    if constexpr (A32 && K64 && WT != T0H_F16 && EPI == EPI_STORE_F32)
+      if (d.M >= 1024) return run_gemm_bf<WT, EPI, 8, true>(d, s);
   }
   if constexpr (!A32 && K64 && WT != T0H_F16) {
     if (tile == 4 && dma_ok(d)) return run_gemm_dma<WT, EPI>(d, s);

@@ -238,3 +238,19 @@ def test_medium_m_forward_epilogues(torch_cuda, t0hip, oracle, rng, qtype, epi, 
     f16 activations and every forward epilogue; one 64-wide K step (fewer steps
     than 32-row slices), the 8-wave limit at K = 4096, ragged M and N."""
     check_forward_gemm(torch_cuda, t0hip, oracle, rng, qtype, 0, epi, m, k, n, sample=False)
+
+
+@pytest.mark.parametrize("qtype", [8, 2])
+@pytest.mark.parametrize("m,k,n", [(1100, 192, 200), (1024, 768, 256), (2049, 64, 37)])
+def test_f32_activations_large_m(torch_cuda, t0hip, oracle, rng, qtype, m, k, n):
+    """t0h_gemm_q at M >= 1024 (f32 activations rounded to f16 while the 256x256
+    register-operand kernel stages them): ragged M and N, an odd number of K
+    steps, one step, bias and ReLU; 1e-2 relative."""
+    W = (0.02 * rng.standard_normal((n, k))).astype(np.float32)
+    x = rng.standard_normal((m, k)).astype(np.float32)
+    b = (0.02 * rng.standard_normal(n)).astype(np.float32)
+    blocks = oracle.quantize(qtype, W)
+    deq = oracle.dequantize(qtype, blocks, n * k).reshape(n, k).astype(np.float64)
+    want = x.astype(np.float64) @ deq.T + b
+    assert rel_err(run_gemm(torch_cuda, t0hip, qtype, blocks, x, b, n), want) < 1e-2
+    assert rel_err(run_gemm(torch_cuda, t0hip, qtype, blocks, x, b, n, act=1), np.maximum(want, 0.0)) < 1e-2
