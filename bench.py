@@ -229,9 +229,11 @@ def cpu_baseline(gguf, x, groups, t_ctx, horizon, budget_s=12.0):
 
 
 # Device kernel behind each profiled GEMM kind of the forward at config 4
-# (template args: weight type 2 = Q4_0 / 8 = Q8_0, epilogue 1 f16 store / 3 SwiGLU).
-KERNEL_OF = {("gemm_w0_swiglu", "q4_0"): "k_gemm_bf<2, 3, 4>", ("gemm_w0_swiglu", "q8_0"): "k_gemm_bf<8, 3, 4>",
-             ("gemm_qkv", "q4_0"): "k_gemm_bf<2, 1, 8>", ("gemm_qkv", "q8_0"): "k_gemm_bf<8, 1, 8>"}
+# (template args: weight type 2 = Q4_0 / 8 = Q8_0, epilogue 1 f16 store / 3 SwiGLU,
+# waves, f32 activations).
+KERNEL_OF = {("gemm_w0_swiglu", "q4_0"): "k_gemm_bf<2, 3, 4, false>",
+             ("gemm_w0_swiglu", "q8_0"): "k_gemm_bf<8, 3, 4, false>",
+             ("gemm_qkv", "q4_0"): "k_gemm_bf<2, 1, 8, false>", ("gemm_qkv", "q8_0"): "k_gemm_bf<8, 1, 8, false>"}
 COPY_BYTES = 256 << 20  # the --calibrate-copy kernel reads and writes this many bytes
 TRAFFIC_FILE = os.path.join(ROOT, "profiles", "traffic_config4.json")
 
