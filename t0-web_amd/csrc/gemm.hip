@@ -1273,8 +1273,9 @@ __global__ __launch_bounds__(256) void k_gemv(const GemmDesc d) {
 
 // ---------------------------------------------------------------------------
 // Medium-M kernel (16 < M < 1024, Q8_0 / Q4_0, K % 64 == 0).  A workgroup owns
-// a 32*TI-row x 32-column output tile (SwiGLU: 16 hidden units in the PAIR
-// layout of k_gemm_bf) and splits K over its waves, KR 64-wide steps each.  A
+// a 32*TI-row x 32*TJ-column output tile (SwiGLU: 16 hidden units in the PAIR
+// layout of k_gemm_bf, TJ = 1) and splits K over its waves, KR 64-wide steps
+// each; each activation fragment feeds the TJ column groups.  A
 // wave issues every load of its K range before the first MFMA: its weight
 // row's blocks in the k_gemm_bf lane layout (lane l holds block l/32 of each
 // step's 2-block span of row l%32, slice c taking k = 32(l/32) + 8c .. +7) and
@@ -1315,39 +1316,44 @@ __device__ __forceinline__ half8 dq_frag(const uint32_t* r, int c, int h) {
   return __builtin_bit_cast(half8, make_uint4(v[0], v[1], v[2], v[3]));
 }
 
-template <int WT, bool A32, int EPI, int TI, int KR>
+template <int WT, bool A32, int EPI, int TI, int KR, int TJ>
 __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2))) void k_gemm_mid(const GemmDesc d) {
   constexpr bool SWI = EPI == EPI_SWIGLU_F16;
   constexpr int NWD = WT == T0H_Q8_0 ? 9 : 5, SWD = WT == T0H_Q8_0 ? 17 : 9;
-  constexpr int W = SWI ? 16 : 32;  // output columns per tile
+  static_assert(!SWI || TJ == 1, "SwiGLU tiles pair gate and up columns in one 32-column group");
+  constexpr int W = SWI ? 16 : 32 * TJ;  // output columns per tile
   extern __shared__ __align__(16) float red[];
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6, nw = blockDim.x >> 6;
   const int h = lane >> 5, lc = lane & 31;
   const int M = d.M, N = d.N, K = d.K, KT = K / 64;
   const int strips = (N + W - 1) / W;
   const int tn = blockIdx.x % strips, m0 = (blockIdx.x / strips) * (32 * TI);
-  int wrow;
-  bool ok;
-  if (SWI) {
-    const int g = tn * 16 + (lc & 15);
-    ok = g < N;
-    wrow = lc < 16 ? g : N + g;
-  } else {
-    wrow = tn * 32 + lc;
-    ok = wrow < N;
-  }
-  // rows past N read row 0, activation rows past M read row M-1 (never stored)
-  const uint32_t* wsrc =
-      static_cast<const uint32_t*>(d.w) + (size_t)(ok ? wrow : 0) * ((K / 32) * block_bytes(WT) / 4) + h * (NWD - 1);
+  // column group j of the tile: the lane's weight row (rows past N read row 0,
+  // activation rows past M read row M-1: never stored)
   const int s0 = wave * KR;
-  uint32_t wr[KR][NWD];
+  uint32_t wr[TJ][KR][NWD];
 #pragma unroll
-  for (int s = 0; s < KR; ++s)
-    if (s0 + s < KT) {
-      const uint32_t* src = wsrc + (s0 + s) * SWD;  // NWD contiguous dwords
-#pragma unroll
-      for (int i = 0; i < NWD; ++i) wr[s][i] = src[i];
+  for (int j = 0; j < TJ; ++j) {
+    int wrow;
+    bool ok;
+    if (SWI) {
+      const int g = tn * 16 + (lc & 15);
+      ok = g < N;
+      wrow = lc < 16 ? g : N + g;
+    } else {
+      wrow = (tn * TJ + j) * 32 + lc;
+      ok = wrow < N;
     }
+    const uint32_t* wsrc =
+        static_cast<const uint32_t*>(d.w) + (size_t)(ok ? wrow : 0) * ((K / 32) * block_bytes(WT) / 4) + h * (NWD - 1);
+#pragma unroll
+    for (int s = 0; s < KR; ++s)
+      if (s0 + s < KT) {
+        const uint32_t* src = wsrc + (s0 + s) * SWD;  // NWD contiguous dwords
+#pragma unroll
+        for (int i = 0; i < NWD; ++i) wr[j][s][i] = src[i];
+      }
+  }
   half8 af[KR][4][TI];
 #pragma unroll
   for (int i = 0; i < TI; ++i) {
@@ -1369,44 +1375,55 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2))) void k
         }
       }
   }
-  floatx16 acc[TI][1];
+  floatx16 acc[TI][TJ];
 #pragma unroll
   for (int i = 0; i < TI; ++i)
 #pragma unroll
-    for (int e = 0; e < 16; ++e) acc[i][0][e] = 0.0f;
+    for (int j = 0; j < TJ; ++j)
+#pragma unroll
+      for (int e = 0; e < 16; ++e) acc[i][j][e] = 0.0f;
 #pragma unroll
   for (int s = 0; s < KR; ++s)
     if (s0 + s < KT) {
 #pragma unroll
-      for (int c = 0; c < 4; ++c) {
-        const half8 b = dq_frag<WT>(wr[s], c, h);
+      for (int c = 0; c < 4; ++c)
 #pragma unroll
-        for (int i = 0; i < TI; ++i) acc[i][0] = __builtin_amdgcn_mfma_f32_32x32x16_f16(af[s][c][i], b, acc[i][0], 0, 0, 0);
-      }
+        for (int j = 0; j < TJ; ++j) {
+          const half8 b = dq_frag<WT>(wr[j][s], c, h);
+#pragma unroll
+          for (int i = 0; i < TI; ++i)
+            acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(af[s][c][i], b, acc[i][j], 0, 0, 0);
+        }
     }
-  // partial tiles: [wave][slice][quad][lane] float4s (lane-contiguous, no bank conflicts)
+  // partial tiles: [wave][slice][group][quad][lane] float4s (lane-contiguous, no bank conflicts)
 #pragma unroll
   for (int i = 0; i < TI; ++i)
 #pragma unroll
-    for (int q = 0; q < 4; ++q)
-      reinterpret_cast<float4*>(red)[((wave * TI + i) * 4 + q) * 64 + lane] =
-          make_float4(acc[i][0][4 * q], acc[i][0][4 * q + 1], acc[i][0][4 * q + 2], acc[i][0][4 * q + 3]);
+    for (int j = 0; j < TJ; ++j)
+#pragma unroll
+      for (int q = 0; q < 4; ++q)
+        reinterpret_cast<float4*>(red)[(((wave * TI + i) * TJ + j) * 4 + q) * 64 + lane] =
+            make_float4(acc[i][j][4 * q], acc[i][j][4 * q + 1], acc[i][j][4 * q + 2], acc[i][j][4 * q + 3]);
   __syncthreads();
   if (wave >= TI) return;
-  floatx16 sum[1][1];
+  floatx16 sum[1][TJ];
 #pragma unroll
-  for (int e = 0; e < 16; ++e) sum[0][0][e] = 0.0f;
+  for (int j = 0; j < TJ; ++j)
+#pragma unroll
+    for (int e = 0; e < 16; ++e) sum[0][j][e] = 0.0f;
   for (int w = 0; w < nw; ++w)
 #pragma unroll
-    for (int q = 0; q < 4; ++q) {
-      const float4 v = reinterpret_cast<const float4*>(red)[((w * TI + wave) * 4 + q) * 64 + lane];
-      sum[0][0][4 * q] += v.x;
-      sum[0][0][4 * q + 1] += v.y;
-      sum[0][0][4 * q + 2] += v.z;
-      sum[0][0][4 * q + 3] += v.w;
-    }
+    for (int j = 0; j < TJ; ++j)
+#pragma unroll
+      for (int q = 0; q < 4; ++q) {
+        const float4 v = reinterpret_cast<const float4*>(red)[(((w * TI + wave) * TJ + j) * 4 + q) * 64 + lane];
+        sum[0][j][4 * q] += v.x;
+        sum[0][j][4 * q + 1] += v.y;
+        sum[0][j][4 * q + 2] += v.z;
+        sum[0][j][4 * q + 3] += v.w;
+      }
   // staging after the partials (other slices may still be reading them)
-  store_tile<EPI, 1, 1>(d, sum, red + nw * TI * 16 * 64, wave, lane, m0 + 32 * wave, tn * W);
+  store_tile<EPI, 1, TJ>(d, sum, red + nw * TI * TJ * 16 * 64, wave, lane, m0 + 32 * wave, tn * W);
 }
 
 // ---------------------------------------------------------------------------
@@ -1706,28 +1723,66 @@ void dispatch_gemv(const GemmDesc& d, hipStream_t s) {
 // Waves of KR steps over K (at most 8 per workgroup, two per SIMD, so a wave
 // may hold its KR steps of operands: up to 256 registers); lds: the partial
 // tiles and the epilogue staging of TI waves.
-template <int WT, bool A32, int EPI, int TI, int KR>
+template <int WT, bool A32, int EPI, int TI, int KR, int TJ = 1>
 void run_gemm_mid(const GemmDesc& d, hipStream_t s) {
   // at least one wave per 32-row slice: slice i is summed and stored by wave i
   const int KT = d.K / 64, nw = std::max(TI, (KT + KR - 1) / KR);
   if (nw > 8) throw Error(T0H_ERR_UNSUPPORTED, "gemm: K too large for the medium-M kernel");
-  const int W = EPI == EPI_SWIGLU_F16 ? 16 : 32;
-  const size_t lds = (size_t)nw * TI * 16 * 64 * 4 + (size_t)TI * 32 * (W + 4) * 4;
+  const int W = EPI == EPI_SWIGLU_F16 ? 16 : 32 * TJ;
+  const size_t lds = (size_t)nw * TI * TJ * 16 * 64 * 4 + (size_t)TI * 32 * (W + 4) * 4;
   const int strips = (d.N + W - 1) / W, mt = (d.M + 32 * TI - 1) / (32 * TI);
-  check_hip(hipFuncSetAttribute(reinterpret_cast<const void*>(&k_gemm_mid<WT, A32, EPI, TI, KR>),
+  check_hip(hipFuncSetAttribute(reinterpret_cast<const void*>(&k_gemm_mid<WT, A32, EPI, TI, KR, TJ>),
                                 hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds),
             "hipFuncSetAttribute(k_gemm_mid)");
-  hipLaunchKernelGGL((k_gemm_mid<WT, A32, EPI, TI, KR>), dim3(strips * mt), dim3(64 * nw), lds, s, d);
+  hipLaunchKernelGGL((k_gemm_mid<WT, A32, EPI, TI, KR, TJ>), dim3(strips * mt), dim3(64 * nw), lds, s, d);
   check_hip(hipGetLastError(), "k_gemm_mid launch");
 }
 
+// Compute units of the current device (the round size of a launch).
+int device_cus() {
+  static int cus[64] = {};
+  int dev = 0;
+  check_hip(hipGetDevice(&dev), "hipGetDevice");
+  if (dev < 0 || dev >= 64) return 256;
+  if (!cus[dev]) {
+    hipDeviceProp_t prop;
+    check_hip(hipGetDeviceProperties(&prop, dev), "hipGetDeviceProperties");
+    cus[dev] = std::max(1, prop.multiProcessorCount);
+  }
+  return cus[dev];
+}
+
 // Shapes the medium-M kernel takes: K % 64 == 0 and K <= 4096 (f16 activations)
-// or 2048 (f32); 32-row tiles for f32 activations or M <= 32, else 64.
+// or 2048 (f32); 32-row tiles for f32 activations or M <= 32, else 64.  From
+// 256 rows (and not SwiGLU) a workgroup may cover four or two 32-column groups
+// (two past K = 1024), so the activation block is read by a quarter or half as
+// many workgroups, when that still fills about one round of the CUs.
 bool mid_ok(const GemmDesc& d) { return d.K % 64 == 0 && d.K <= (d.a_f32 ? 2048 : 4096); }
+
+// Workgroups of a TJ-group launch with 32-row tiles, and whether they fill
+// between three quarters of a round and one round of the device's CUs (the
+// LDS of the partial tiles bounds the workgroups per CU).
+bool mid_groups_fit(const GemmDesc& d, int tj, int kr) {
+  const int KT = d.K / 64, nw = std::max(1, (KT + kr - 1) / kr), cus = device_cus();
+  const long long wgs = (long long)((d.N + 32 * tj - 1) / (32 * tj)) * ((d.M + 31) / 32);
+  const size_t lds = (size_t)nw * tj * 16 * 64 * 4 + (size_t)32 * (32 * tj + 4) * 4;
+  const long long per_cu = std::max<long long>(1, (long long)(160 * 1024 / lds));
+  return nw <= 8 && wgs * 4 >= 3LL * cus && wgs <= per_cu * cus;
+}
 
 template <int WT, bool A32, int EPI>
 void dispatch_mid(const GemmDesc& d, hipStream_t s) {
   const int KT = d.K / 64;
+  if constexpr (EPI != EPI_SWIGLU_F16) {
+    if (d.M >= 256 && KT <= 32) {
+      const int kr = KT <= 16 ? 2 : 4;
+      if (kr == 2 && mid_groups_fit(d, 4, 2)) return run_gemm_mid<WT, A32, EPI, 1, 2, 4>(d, s);
+      if (mid_groups_fit(d, 2, kr)) {  // (4 groups x 4 steps of Q8_0 spans spill)
+        if (kr == 2) return run_gemm_mid<WT, A32, EPI, 1, 2, 2>(d, s);
+        return run_gemm_mid<WT, A32, EPI, 1, 4, 2>(d, s);
+      }
+    }
+  }
   if (A32 || d.M <= 32 || KT > 32) {
     if (KT <= 16) return run_gemm_mid<WT, A32, EPI, 1, 2>(d, s);
     if (KT <= 32) return run_gemm_mid<WT, A32, EPI, 1, 4>(d, s);

@@ -232,11 +232,12 @@ def test_small_m_forward_epilogues(torch_cuda, t0hip, oracle, rng, qtype, epi, m
 
 @pytest.mark.parametrize("qtype", [8, 2])
 @pytest.mark.parametrize("epi", [0, 1, 2, 3])
-@pytest.mark.parametrize("m,k,n", [(17, 768, 136), (66, 2048, 72), (300, 64, 40), (1000, 4096, 48)])
+@pytest.mark.parametrize("m,k,n", [(17, 768, 136), (66, 2048, 72), (300, 64, 40), (260, 2048, 200), (1000, 4096, 48)])
 def test_medium_m_forward_epilogues(torch_cuda, t0hip, oracle, rng, qtype, epi, m, k, n):
     """The medium-M kernel (16 < M < 1024, K split over the waves of a workgroup):
     f16 activations and every forward epilogue; one 64-wide K step (fewer steps
-    than 32-row slices), the 8-wave limit at K = 4096, ragged M and N."""
+    than 32-row slices), four and two 32-column groups per workgroup (M >= 256),
+    the 8-wave limit at K = 4096, ragged M and N."""
     check_forward_gemm(torch_cuda, t0hip, oracle, rng, qtype, 0, epi, m, k, n, sample=False)
 
 
