@@ -233,7 +233,7 @@ def cpu_baseline(gguf, x, groups, t_ctx, horizon, budget_s=12.0):
 # waves, f32 activations).
 KERNEL_OF = {("gemm_w0_swiglu", "q4_0"): "k_gemm_bf<2, 3, 4, false>",
              ("gemm_w0_swiglu", "q8_0"): "k_gemm_bf<8, 3, 4, false>",
-             ("gemm_qkv", "q4_0"): "k_gemm_bf<2, 1, 8, false>", ("gemm_qkv", "q8_0"): "k_gemm_bf<8, 1, 8, false>"}
+             ("gemm_qkv", "q4_0"): "k_gemm_bf<2, 1, 4, false>", ("gemm_qkv", "q8_0"): "k_gemm_bf<8, 1, 4, false>"}
 COPY_BYTES = 256 << 20  # the --calibrate-copy kernel reads and writes this many bytes
 TRAFFIC_FILE = os.path.join(ROOT, "profiles", "traffic_config4.json")
 

@@ -1645,12 +1645,14 @@ void run_gemm_tiled(const GemmDesc& d, int tile, hipStream_t s) {
   // By shape (tile 0).  Measured at the config-4 layer shapes (M = 50,688,
   // Q4_0, us; register-operand 256x128 at two workgroups per CU / 256x256 /
   // 128x128): SwiGLU 360 / 363 / 430, QKV 250 / 245 / 290, wO 97 / 103 / 107,
-  // w2 224 / 232 / 238.  The DMA and plain 256x256 tiles lose at every shape.
+  // w2 224 / 232 / 238 (standalone).  Inside the forward QKV measured 213.5 us
+  // on the 256x128 kernel against 217.5 on the 256x256 one, so it takes the
+  // 256x128 kernel too.  The DMA and plain 256x256 tiles lose at every shape.
   // Below ~1024 rows a 256-row tile is mostly padding.
   if (tile == 0) {
     tile = 1;
     if constexpr (!A32 && K64 && WT != T0H_F16)
-      if (d.M >= 1024) tile = EPI != EPI_SWIGLU_F16 && d.N >= 1536 ? 5 : 6;
+      if (d.M >= 1024) tile = 6;
     // f32 activations (f32 stores only): the 256x256 register-operand kernel
     // converts them while staging
     if constexpr (A32 && K64 && WT != T0H_F16 && EPI == EPI_STORE_F32)
