@@ -220,6 +220,64 @@ __device__ __forceinline__ void store_tile(const GemmDesc& d, floatx16 (&acc)[TI
     b1[j] = (SWI && ok) ? d.bias[N + col] : 0.0f;
   }
   const bool vec_ok = (d.ldy & 3) == 0 && (N & 3) == 0;
+  // f16 outputs of one column group (the register-operand and medium-M
+  // kernels) in 16-byte chunks: adjacent columns sit in lanes l and l^1 with the
+  // same rows, so one DPP swap pairs them into f16 dwords; each slice is staged
+  // as f16 (half the LDS traffic of the f32 stage) and stored 8 columns a lane.
+  constexpr bool F16P = PAIR || (EPI == EPI_STORE_F16 && TJ == 1);
+  if constexpr (F16P) {
+    const bool vec8 = (d.ldy & 7) == 0 && (N & 7) == 0 && (reinterpret_cast<uintptr_t>(d.y) & 15) == 0;
+    if (vec8) {
+      constexpr int WD = W / 2, SH = WD + 4;  // f16 dwords per staged row (+4: 16-byte aligned rows)
+      constexpr int CPR = WD / 4;             // 16-byte chunks per row
+      static_assert(SH <= SLD, "f16 stage fits the f32 stage");
+      uint32_t* st = reinterpret_cast<uint32_t*>(stage);
+      const int odd = lc & 1;
+      auto pack = [&](float mine, float nb) {
+        const half2v pr = odd ? half2v{(_Float16)nb, (_Float16)mine} : half2v{(_Float16)mine, (_Float16)nb};
+        return __builtin_bit_cast(uint32_t, pr);
+      };
+#pragma unroll
+      for (int i = 0; i < TI; ++i) {
+        if constexpr (PAIR) {
+          // result k of lane l: unit l%16, row of e = 2k + (l%32)/16 (as below)
+          float v[8];
+#pragma unroll
+          for (int k = 0; k < 8; ++k) {
+            const auto gu = __builtin_amdgcn_permlane16_swap(__float_as_uint(acc[i][0][2 * k]),
+                                                             __float_as_uint(acc[i][0][2 * k + 1]), false, false);
+            v[k] = silu(__uint_as_float(gu[0]) + b0[0]) * (__uint_as_float(gu[1]) + b1[0]);
+          }
+#pragma unroll
+          for (int k = 0; k < 8; ++k) {
+            const float nb = dpp_move<0xB1>(v[k]);  // lane l^1
+            if ((k & 1) == odd) {
+              const int ee = 2 * k + (lc >> 4);
+              st[((ee >> 2) * 8 + lr + (ee & 3)) * SH + (uc >> 1)] = pack(v[k], nb);
+            }
+          }
+        } else {
+#pragma unroll
+          for (int e = 0; e < 16; ++e) {
+            float v = acc[i][0][e] + b0[0];
+            if (d.relu) v = fmaxf(v, 0.0f);
+            const float nb = dpp_move<0xB1>(v);  // lane l^1
+            if ((e & 1) == odd) st[((e >> 2) * 8 + lr + (e & 3)) * SH + (lc >> 1)] = pack(v, nb);
+          }
+        }
+        const int row0 = row_base + i * 32;
+#pragma unroll
+        for (int t = 0; t < 32 * CPR / 64; ++t) {
+          const int idx = t * 64 + lane, r = idx / CPR, c = idx % CPR;
+          const int row = row0 + r, col = cbase + c * 8;
+          if (row < M && col < N)
+            *reinterpret_cast<uint4*>(static_cast<_Float16*>(d.y) + (size_t)row * d.ldy + col) =
+                *reinterpret_cast<const uint4*>(st + r * SH + c * 4);
+        }
+      }
+      return;
+    }
+  }
   // Residual: the old values of a 32-row slice are loaded one slice ahead, so
   // the read-modify-writes do not wait on a memory round trip each.
   // (Wide waves, NT > 8, load each slice's own values before staging it.)
