@@ -249,3 +249,26 @@ def test_config5_full_size(t0hip, oracle, engine, rng):
     om = oracle.Model(g)
     want = om.forecast_grouped(ctx[:v], groups[:v], t_ctx, h)
     assert_close(full[:v, :h], want, scale=scale)
+
+
+def test_config4_full_size(t0hip, oracle, engine, rng):
+    """BASELINE config 4 at full size, as bench.py times it: 256 series x 3 variates (one group id
+    per series), ctx 2048, horizon 64, sine mixture x lognormal scale with 10% NaN gaps in runs of
+    16-128, Q4_0 BASELINE model; 50,688 patch rows, so every layer GEMM runs the register-operand
+    MFMA kernel.  Two series of the full batch against the oracle (5e-3 of each row's scale), and
+    batch isolation: series 0 alone gives the same forecast (its 66 rows take the medium-M kernel)."""
+    n_series, v, t_ctx, h = 256, 3, 2048, 64
+    g = t0hip.synth_model_gguf(t0hip.make_config(**BASELINE), quant=2, seed=0)
+    gm = t0hip.load_model_from_gguf(engine, g)
+    x = sine_mix(rng, n_series * v, t_ctx) * np.repeat(np.exp(rng.standard_normal(n_series)), v)[:, None].astype(np.float32)
+    x = nan_gaps(rng, x)
+    groups = np.repeat(np.arange(n_series), v).astype(np.int64)
+    full = t0hip.forecast_grouped(engine, gm, x, groups, t_ctx, h)
+    assert full.shape == (n_series * v, h, 9) and np.isfinite(full).all()
+    om = oracle.Model(g)
+    for s in (0, 137):
+        rows = slice(s * v, (s + 1) * v)
+        want = om.forecast_grouped(x[rows], groups[rows], t_ctx, h)
+        assert_close(full[rows], want, scale=row_scale(x[rows]))
+    alone = t0hip.forecast_grouped(engine, gm, x[:v], groups[:v], t_ctx, h)
+    assert_close(full[:v], alone, scale=row_scale(x[:v]))
