@@ -256,7 +256,9 @@ def test_config4_full_size(t0hip, oracle, engine, rng):
     per series), ctx 2048, horizon 64, sine mixture x lognormal scale with 10% NaN gaps in runs of
     16-128, Q4_0 BASELINE model; 50,688 patch rows, so every layer GEMM runs the register-operand
     MFMA kernel.  Two series of the full batch against the oracle (5e-3 of each row's scale), and
-    batch isolation: series 0 alone gives the same forecast (its 66 rows take the medium-M kernel)."""
+    batch isolation: series 0 alone (its 198 rows take the medium-M kernel) gives the same forecast
+    up to 1e-2, the sum of the two paths' allowed distances from the oracle (each is checked
+    against it at 5e-3; rows leaking across series would differ by order 1)."""
     n_series, v, t_ctx, h = 256, 3, 2048, 64
     g = t0hip.synth_model_gguf(t0hip.make_config(**BASELINE), quant=2, seed=0)
     gm = t0hip.load_model_from_gguf(engine, g)
@@ -271,4 +273,5 @@ def test_config4_full_size(t0hip, oracle, engine, rng):
         want = om.forecast_grouped(x[rows], groups[rows], t_ctx, h)
         assert_close(full[rows], want, scale=row_scale(x[rows]))
     alone = t0hip.forecast_grouped(engine, gm, x[:v], groups[:v], t_ctx, h)
-    assert_close(full[:v], alone, scale=row_scale(x[:v]))
+    assert_close(alone, om.forecast_grouped(x[:v], groups[:v], t_ctx, h), scale=row_scale(x[:v]))
+    assert_close(full[:v], alone, scale=row_scale(x[:v]), tol=2 * TOL)
