@@ -121,6 +121,11 @@ int t0h_model_workspace(const t0h_model* model, uint64_t* resident_bytes, uint64
  * recording; 0 stops.  Entries are indexed 0..n-1 in first-seen order; an index
  * past the end returns T0H_ERR_INVALID_ARG. */
 int t0h_model_profile(t0h_model* model, int enable);
+/* As t0h_model_profile(model, 1), but times only the launches of one kernel kind
+ * (a name t0h_model_profile_entry reports), so that the events cost the forward
+ * two records per launch of that kind and nothing elsewhere.  Stop with
+ * t0h_model_profile(model, 0). */
+int t0h_model_profile_kind(t0h_model* model, const char* kind);
 int t0h_model_profile_entry(t0h_model* model, size_t i, char* name, size_t name_cap, uint64_t* launches,
                             double* total_ms);
 

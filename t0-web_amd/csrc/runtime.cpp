@@ -87,6 +87,7 @@ struct ProfEntry {
 };
 struct Profiler {
   bool on = false;
+  std::string only;  // when non-empty, only launches of this kind are timed
   std::vector<ProfEntry> entries;
   std::vector<hipEvent_t> spare;
 };
@@ -194,6 +195,7 @@ struct ProfScope {
   hipEvent_t start = nullptr;
   ProfScope(t0h_model* model, const char* name) : m(model) {
     if (!m->prof.on) return;
+    if (!m->prof.only.empty() && m->prof.only != name) return;
     auto& es = m->prof.entries;
     idx = es.size();
     for (size_t i = 0; i < es.size(); ++i)
@@ -940,6 +942,22 @@ int t0h_model_profile(t0h_model* m, int enable) {
     e.total_ms = 0.0;
   }
   m->prof.on = enable != 0;
+  m->prof.only.clear();
+  API_END
+}
+
+int t0h_model_profile_kind(t0h_model* m, const char* kind) {
+  API_BEGIN
+  require(m != nullptr && kind != nullptr, "t0h_model_profile_kind: NULL argument");
+  require(kind[0] != '\0', "t0h_model_profile_kind: empty kind");
+  bind_device(m);
+  prof_collect(m);
+  for (auto& e : m->prof.entries) {
+    e.launches = 0;
+    e.total_ms = 0.0;
+  }
+  m->prof.on = true;
+  m->prof.only = kind;
   API_END
 }
 

@@ -73,7 +73,7 @@ _lib = None
 SYMBOLS = [
     "t0h_last_error", "t0h_abi_version", "t0h_ctx_create", "t0h_ctx_destroy", "t0h_gguf_inspect",
     "t0h_model_load_gguf", "t0h_model_destroy", "t0h_model_config", "t0h_model_weight_bytes", "t0h_model_stream",
-    "t0h_model_workspace", "t0h_model_profile", "t0h_model_profile_entry", "t0h_forward", "t0h_forecast", "t0h_forecast_batch_chunked",
+    "t0h_model_workspace", "t0h_model_profile", "t0h_model_profile_kind", "t0h_model_profile_entry", "t0h_forward", "t0h_forecast", "t0h_forecast_batch_chunked",
     "t0h_forecast_batch_rows_chunked", "t0h_forecast_grouped", "t0h_forecast_grouped_dev",
     "t0h_forecast_grouped_ar", "t0h_forecast_rollout", "t0h_dequant", "t0h_gemm_q", "t0h_gemm_f16", "t0h_row_bytes",
     "t0h_quantize", "t0h_synth_model_gguf", "t0h_export_gguf",
@@ -105,6 +105,7 @@ def lib():
     L.t0h_model_stream.argtypes = [P]
     L.t0h_model_workspace.argtypes = [P, C.POINTER(C.c_uint64), C.POINTER(C.c_uint64)]
     L.t0h_model_profile.argtypes = [P, I]
+    L.t0h_model_profile_kind.argtypes = [P, C.c_char_p]
     L.t0h_model_profile_entry.argtypes = [P, S, C.c_char_p, S, C.POINTER(C.c_uint64), C.POINTER(C.c_double)]
     L.t0h_forward.argtypes = [P, C.POINTER(Series), P, S, P, P]
     L.t0h_forecast.argtypes = [P, P, S, S, S, P, S]
@@ -207,13 +208,14 @@ class Engine:
     """≡ t0_fast::Engine (crates/t0-fast/src/engine.rs:18-44): one GPU, shareable by models."""
 
     def __init__(self, device=0):
+        self._lib = lib()  # held so that close() still reaches it while the interpreter exits
         h = C.c_void_p()
-        _check(lib().t0h_ctx_create(device, C.byref(h)))
+        _check(self._lib.t0h_ctx_create(device, C.byref(h)))
         self.h = h
 
     def close(self):
         if getattr(self, "h", None):
-            lib().t0h_ctx_destroy(self.h)
+            self._lib.t0h_ctx_destroy(self.h)
             self.h = None
 
     def __del__(self):
@@ -226,6 +228,7 @@ class GpuModel:
 
     def __init__(self, engine, gguf_bytes):
         self.engine = engine  # keep the context alive
+        self._lib = lib()
         self._bytes = np.frombuffer(bytes(gguf_bytes), np.uint8)
         h = C.c_void_p()
         _check(lib().t0h_model_load_gguf(engine.h, _p(self._bytes), self._bytes.size, C.byref(h)))
@@ -236,7 +239,7 @@ class GpuModel:
 
     def close(self):
         if getattr(self, "h", None):
-            lib().t0h_model_destroy(self.h)
+            self._lib.t0h_model_destroy(self.h)
             self.h = None
 
     def __del__(self):
@@ -263,6 +266,10 @@ class GpuModel:
     def profile(self, enable=True):
         """Start (reset) or stop per-kernel-kind event timing of this model's forward."""
         _check(lib().t0h_model_profile(self.h, int(enable)))
+
+    def profile_kind(self, kind):
+        """Start (reset) event timing of the launches of one kernel kind only; stop with profile(False)."""
+        _check(lib().t0h_model_profile_kind(self.h, kind.encode()))
 
     def profile_report(self):
         """{kernel kind: (launches, total_ms)} recorded since profile(True)."""

@@ -198,6 +198,36 @@ def test_error_paths_on_device(models, t0hip, engine, rng):
     assert e.value.status == "INVALID_ARG"
 
 
+def test_profiler_all_kinds_and_one_kind(models, t0hip, engine, rng):
+    """Event timing of every kernel kind, then of one kind only: the one-kind run times the
+    same launches of that kind and nothing else, and neither changes the forecast."""
+    gm, _ = models[("tiny", 8)]
+    layers = TINY["num_layers"]
+    ctx = sine_mix(rng, 3, 256)
+    want = t0hip.forecast(engine, gm, ctx, 3, 256, 32)
+    gm.profile(True)
+    got = t0hip.forecast(engine, gm, ctx, 3, 256, 32)
+    full = gm.profile_report()
+    gm.profile(False)
+    assert np.array_equal(got, want)
+    n_sw, ms_sw = full["gemm_w0_swiglu"]
+    assert n_sw > 0 and n_sw % layers == 0 and ms_sw > 0
+    assert sum(1 for n, _ in full.values() if n) >= 5
+    gm.profile_kind("gemm_w0_swiglu")
+    got = t0hip.forecast(engine, gm, ctx, 3, 256, 32)
+    one = gm.profile_report()
+    gm.profile(False)
+    assert np.array_equal(got, want)
+    assert one["gemm_w0_swiglu"][0] == n_sw and one["gemm_w0_swiglu"][1] > 0
+    assert all(n == 0 for k, (n, _) in one.items() if k != "gemm_w0_swiglu")
+    # stopped: a further forward records nothing
+    t0hip.forecast(engine, gm, ctx, 3, 256, 32)
+    assert all(n == 0 for n, _ in gm.profile_report().values())
+    with pytest.raises(t0hip.T0HipError) as e:
+        gm.profile_kind("")
+    assert e.value.status == "INVALID_ARG"
+
+
 def test_baseline_model_forecast(t0hip, oracle, engine, rng):
     """The BASELINE synthetic model (12 layers, embed 768, Q8_0), config 3 input: one series,
     sum of 3 sines + N(0, 0.1), context 2048, horizon 64."""
