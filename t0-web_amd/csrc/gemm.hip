@@ -198,10 +198,24 @@ __device__ __forceinline__ void dq_chunk(const uint32_t (&br)[16], int part, int
 // wave writes TJ*16 output columns from cbase; otherwise TJ*32.  `smemf` needs
 // (waves) * 32 * (W + 4) floats and must be free (callers end their main loop
 // with a barrier).
-template <int EPI, int TI, int TJ>
+// Bias of the one column a lane writes when a wave has one column group (b1:
+// the up half of SwiGLU; 0 past N or without bias), for kernels that load it
+// before their main loop and hand it to store_tile (PRE) so that the epilogue
+// does not start with a memory round trip.
+template <int EPI>
+__device__ __forceinline__ void tile_bias1(const GemmDesc& d, int lane, int cbase, float& b0, float& b1) {
+  const int lc = lane & 31, col = cbase + (EPI == EPI_SWIGLU_F16 ? (lc & 15) : lc);
+  const bool ok = d.bias && col < d.N;
+  b0 = ok ? d.bias[col] : 0.0f;
+  b1 = (EPI == EPI_SWIGLU_F16 && ok) ? d.bias[d.N + col] : 0.0f;
+}
+
+template <int EPI, int TI, int TJ, bool PRE = false>
 __device__ __forceinline__ void store_tile(const GemmDesc& d, floatx16 (&acc)[TI][TJ], float* smemf, int wave,
-                                           int lane, int row_base, int cbase) {
+                                           int lane, int row_base, int cbase, float pre0 = 0.0f,
+                                           float pre1 = 0.0f) {
   constexpr bool SWI = EPI == EPI_SWIGLU_F16;
+  static_assert(!PRE || TJ == 1, "a preloaded bias covers one column group");
   // SwiGLU with one column group (PAIR): lanes l%32 < 16 hold the gate and
   // lanes l%32 >= 16 the up column of the same 16 hidden units.
   constexpr bool PAIR = SWI && TJ == 1;
@@ -212,12 +226,17 @@ __device__ __forceinline__ void store_tile(const GemmDesc& d, floatx16 (&acc)[TI
   float* stage = smemf + wave * 32 * SLD;
   const int lc = lane & 31, lr = (lane >> 5) * 4, uc = PAIR ? (lc & 15) : lc;
   float b0[NJ], b1[NJ];
+  if constexpr (PRE) {
+    b0[0] = pre0;
+    b1[0] = pre1;
+  } else {
 #pragma unroll
-  for (int j = 0; j < NJ; ++j) {
-    const int col = cbase + j * 32 + uc;
-    const bool ok = d.bias && col < N;
-    b0[j] = ok ? d.bias[col] : 0.0f;
-    b1[j] = (SWI && ok) ? d.bias[N + col] : 0.0f;
+    for (int j = 0; j < NJ; ++j) {
+      const int col = cbase + j * 32 + uc;
+      const bool ok = d.bias && col < N;
+      b0[j] = ok ? d.bias[col] : 0.0f;
+      b1[j] = (SWI && ok) ? d.bias[N + col] : 0.0f;
+    }
   }
   const bool vec_ok = (d.ldy & 3) == 0 && (N & 3) == 0;
   // f16 outputs of one column group (the register-operand and medium-M
@@ -1065,6 +1084,14 @@ __global__ __launch_bounds__(64 * NWV) __attribute__((amdgpu_waves_per_eu(2, 2))
     for (int e = 0; e < 4; ++e) asm volatile("" : "+v"(ts[e]));
   };
 
+  // The residual epilogues (wO, w2) load their bias before the main loop:
+  // measured 2 us faster on wO; the f16 and SwiGLU epilogues measured ~1.5 us
+  // slower with it and load theirs in store_tile.
+  constexpr bool PREB = EPI == EPI_RESID_F32;
+  const int cbase = SWI ? tn * HB + wave * 16 : tn * BN + wave * 32;
+  float pb0 = 0.0f, pb1 = 0.0f;
+  if constexpr (PREB) tile_bias1<EPI>(d, lane, cbase, pb0, pb1);
+
   floatx16 acc[TI][TJ];
 #pragma unroll
   for (int i = 0; i < TI; ++i)
@@ -1153,8 +1180,7 @@ __global__ __launch_bounds__(64 * NWV) __attribute__((amdgpu_waves_per_eu(2, 2))
   }
   if (kt < KT) step(kt, wr0, wr1);
 
-  store_tile<EPI, TI, TJ>(d, acc, reinterpret_cast<float*>(smem), wave, lane, m0,
-                          SWI ? tn * HB + wave * 16 : tn * BN + wave * 32);
+  store_tile<EPI, TI, TJ, PREB>(d, acc, reinterpret_cast<float*>(smem), wave, lane, m0, cbase, pb0, pb1);
 }
 
 // ---------------------------------------------------------------------------
