@@ -242,6 +242,18 @@ def test_medium_m_forward_epilogues(torch_cuda, t0hip, oracle, rng, qtype, epi, 
 
 
 @pytest.mark.parametrize("qtype", [8, 2])
+@pytest.mark.parametrize("epi", [0, 1, 2, 3])
+@pytest.mark.parametrize("m,k,n", [(1023, 768, 96), (1024, 768, 96), (512, 768, 2304), (513, 768, 2304),
+                                   (600, 2048, 2000)])
+def test_forward_dispatch_boundaries(torch_cuda, t0hip, oracle, rng, qtype, epi, m, k, n):
+    """The automatic kernel choice (tile 0) on both sides of each boundary with
+    every forward epilogue: the medium-M kernel up to M = 1023 and up to 512 x 2304
+    outputs, the register-operand kernel from M = 1024, the LDS-staged kernel for
+    medium M past 512 x 2304 outputs (513 x 2304, 600 x 2000)."""
+    check_forward_gemm(torch_cuda, t0hip, oracle, rng, qtype, 0, epi, m, k, n, sample=False)
+
+
+@pytest.mark.parametrize("qtype", [8, 2])
 @pytest.mark.parametrize("m,k,n", [(1100, 192, 200), (1024, 768, 256), (2049, 64, 37)])
 def test_f32_activations_large_m(torch_cuda, t0hip, oracle, rng, qtype, m, k, n):
     """t0h_gemm_q at M >= 1024 (f32 activations rounded to f16 while the 256x256
