@@ -164,10 +164,16 @@ __global__ __launch_bounds__(256) void k_prep_rows(const WindowDesc w, const Pat
   float* pl = scv + t;         // [p] loc at patch end
   float* psc = pl + p;         // [p] scale at patch end
   Wf* st = reinterpret_cast<Wf*>(psc + p);  // [2][256] scan buffers
+  // [t] step masks: the later passes read them here instead of calling
+  // window_step again (a dependent global load per step; one row's patch
+  // metadata loop alone took about 20 us that way).  A step's group is the
+  // row's and its type TARGET unless the step is PAD (group and type -1).
+  unsigned char* smask = reinterpret_cast<unsigned char*>(st + 2 * 256);
 
   for (int s = tid; s < t; s += 256) {
     const Step stp = window_step(w, r, s);
     xs[s] = stp.mask == T0H_MASK_VALID ? stp.x : NAN;
+    smask[s] = (unsigned char)stp.mask;
   }
   __syncthreads();
   const int C = (t + 255) / 256;
@@ -206,7 +212,7 @@ __global__ __launch_bounds__(256) void k_prep_rows(const WindowDesc w, const Pat
     const float var = state.n > 1.0f ? fmaxf(state.m2 / (state.n - 1.0f), 0.0f) : 0.0f;
     float sc = w.variance_offset ? sqrtf(var + w.eps) : fmaxf(sqrtf(var), w.eps);
     float lc = state.mean;
-    if (window_step(w, r, s).group < 0) {  // padding sentinel (scaler.rs:56-62)
+    if (smask[s] == T0H_MASK_PAD) {  // padding sentinel, group < 0 (scaler.rs:56-62)
       lc = 0.0f;
       sc = 1.0f;
     }
@@ -231,11 +237,13 @@ __global__ __launch_bounds__(256) void k_prep_rows(const WindowDesc w, const Pat
       val = isnan(xs[pi * ps + f - 2 * ps]) ? 0.0f : 1.0f;
     enc[idx] = (_Float16)val;
   }
+  const int g = w.group[r];
   for (int pi = tid; pi < p; pi += 256) {
     PatchAcc acc;
     for (int k = 0; k < ps; ++k) {
-      const Step stp = window_step(w, r, pi * ps + k);
-      acc.add(stp.mask, stp.group, stp.type);
+      const int mk = smask[pi * ps + k];
+      const bool pad = mk == T0H_MASK_PAD;
+      acc.add(mk, pad ? -1 : g, pad ? -1 : T0H_VT_TARGET);
     }
     write_patch_meta(o, m0 + pi, acc);
     if (o.patch_loc) {
@@ -246,7 +254,9 @@ __global__ __launch_bounds__(256) void k_prep_rows(const WindowDesc w, const Pat
   }
 }
 
-size_t prep_lds(int t, int ps) { return (size_t)(2 * t + 2 * (t / ps)) * 4 + 2 * 256 * sizeof(Wf); }
+size_t prep_lds(int t, int ps) {
+  return (size_t)(2 * t + 2 * (t / ps)) * 4 + 2 * 256 * sizeof(Wf) + (size_t)(t + 3) / 4 * 4;
+}
 
 __global__ __launch_bounds__(256) void k_series_patchify(const SeriesDev sd, const PatchOut o) {
   const int p = sd.t / sd.ps;
