@@ -1110,10 +1110,17 @@ __global__ __launch_bounds__(64 * NWV) __attribute__((amdgpu_waves_per_eu(2, 2))
   // (W first when the ACH = 8 chunk loads would push it into the second
   // slice: its data is needed in the last), the activation stores in the
   // last slice.
+  //
+  // With two buffers (EARLY), a chunk's load for step kt+2 is issued right
+  // after its store for step kt+1, so a load has a whole step and the barrier
+  // to land instead of three slices (QKV 2.6, w2 3.5, SwiGLU 1.6 us faster at
+  // config 4).  Q8_0 SwiGLU keeps the loads in the first slice: the longer
+  // live range spills there.
   constexpr int WPOS = ACH < TI ? ACH : 0, A0 = ACH < TI ? 0 : 1;
+  constexpr bool EARLY = NBUF == 2 && !(WT == T0H_Q8_0 && SWI);
   auto step = [&](int kt, uint32_t (&cur)[NWD], uint32_t (&nxt)[NWD]) {
     const int b1 = abuf + 1 == NBUF ? 0 : abuf + 1, b2 = b1 + 1 == NBUF ? 0 : b1 + 1;
-    const int kb = min(kt + 1, last), ka = min(kt + NBUF - 1, last);
+    const int kb = min(kt + 1, last), ka = min(kt + NBUF - 1, last), ka2 = min(kt + 2, last);
     if constexpr (NBUF == 2) {
 #pragma unroll
       for (int m = 0; m < RD; ++m) ring[m] = read_a(abuf, m / TI, m % TI);
@@ -1130,14 +1137,17 @@ __global__ __launch_bounds__(64 * NWV) __attribute__((amdgpu_waves_per_eu(2, 2))
         else if (NBUF == 3)
           ring[mr % RING] = read_a(b1, 0, mr - NMI);
         if (m == WPOS) load_b(nxt, kb);
-        if (m >= A0 && m < A0 + ACH) load_a(ar[m - A0], ka, m - A0);
+        if (!EARLY && m >= A0 && m < A0 + ACH) load_a(ar[m - A0], ka, m - A0);
         if ((i & 1) == 0) {
           if (c < 3)
             dq(cur, c + 1, i >> 1, bf[n]);
           else
             dq(nxt, 0, i >> 1, bf[n]);
         }
-        if (c == 3 && i < ACH) *a_dst(NBUF == 3 ? b2 : b1, i) = a_f16(ar[i]);
+        if (c == 3 && i < ACH) {
+          *a_dst(NBUF == 3 ? b2 : b1, i) = a_f16(ar[i]);
+          if (EARLY) load_a(ar[i], ka2, i);
+        }
         __builtin_amdgcn_sched_barrier(0);
       }
     }
@@ -1146,7 +1156,8 @@ __global__ __launch_bounds__(64 * NWV) __attribute__((amdgpu_waves_per_eu(2, 2))
   };
 
   // Prologue: A(0) (and, with three buffers, A(1)) into the first buffers,
-  // W(0), the first ring fragments and the slice-0 B fragment.
+  // W(0), the first ring fragments and the slice-0 B fragment; EARLY: A(1)
+  // into the chunk registers.
   {
     AR ar1[ACH];
 #pragma unroll
@@ -1161,6 +1172,10 @@ __global__ __launch_bounds__(64 * NWV) __attribute__((amdgpu_waves_per_eu(2, 2))
     if constexpr (NBUF == 3) {
 #pragma unroll
       for (int q = 0; q < ACH; ++q) *a_dst(1, q) = a_f16(ar1[q]);
+    }
+    if constexpr (EARLY) {
+#pragma unroll
+      for (int q = 0; q < ACH; ++q) load_a(ar[q], min(1, last), q);
     }
   }
   __syncthreads();
