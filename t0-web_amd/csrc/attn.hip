@@ -166,18 +166,25 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(MAXKT <= 8 
 
   const bool fut = d.fut[r] != 0;
   _Float16* ost = Os + wave * 16 * LDH;
-  for (int k = 0;; ++k) {
-    const int qt = tile_at(k);
-    if (qt < 0) break;
-    const int qi = qt * 16 + (lane & 15);
-    float ta[16], tb[16];
-    if (qi < p) {
-      const float* t = d.rope_q + (size_t)qi * 128 + part * 8;
+  // A query tile's rows of the q table (norm scale x rotation x xpos scale);
+  // the next tile's are loaded after this tile's PV products, so they arrive
+  // during the output stores instead of at the head of the tile.
+  float ta[16], tb[16];
+  auto load_t = [&](int qt2) {
+    const int q2 = qt2 * 16 + (lane & 15);
+    if (qt2 >= 0 && q2 < p) {
+      const float* t = d.rope_q + (size_t)q2 * 128 + part * 8;
       load_f8(t, ta);
       load_f8(t + 32, ta + 8);
       load_f8(t + 64, tb);
       load_f8(t + 96, tb + 8);
     }
+  };
+  load_t(tile_at(0));
+  for (int k = 0;; ++k) {
+    const int qt = tile_at(k);
+    if (qt < 0) break;
+    const int qi = qt * 16 + (lane & 15);
     uint4 na, nc;  // the next tile's queries, in flight during this tile
     load_q(tile_at(k + 1), na, nc);
     float x[16];
@@ -263,6 +270,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(MAXKT <= 8 
         }
       }
     }
+    load_t(tile_at(k + 1));
     // Stage O (16 queries x 64 dims) in the wave's own region, then write
     // 16-byte row chunks.  LDS operations of one wave complete in order; the
     // fences keep the compiler from moving the reads above the writes.
