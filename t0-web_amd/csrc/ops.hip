@@ -43,20 +43,22 @@ __global__ __launch_bounds__(256) void k_rmsnorm(const float* x, const float* sc
   }
 }
 
-// Rows up to 1024 wide: the wave holds its row in registers (one memory round
-// trip), sums over DPP lane moves and row swaps, normalizes from registers.
+// Rows up to 1024 wide: the wave holds its row and the scale in registers (one
+// memory round trip), sums over DPP lane moves and row swaps, normalizes from
+// registers.
 __global__ __launch_bounds__(256) void k_rmsnorm_reg(const float* x, const float* scale, _Float16* out,
                                                      const int* map, int rows, int dim) {
   const int lane = threadIdx.x & 63;
   const int row = blockIdx.x * 4 + (threadIdx.x >> 6);
   if (row >= rows) return;
   const float* src = x + (size_t)(map ? map[row] : row) * dim;
-  float4 v[4];
+  float4 v[4], g[4];
   float ss = 0.0f;
 #pragma unroll
   for (int j = 0; j < 4; ++j) {
     const int c = lane * 4 + j * 256;
     v[j] = c < dim ? *reinterpret_cast<const float4*>(src + c) : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+    g[j] = c < dim ? *reinterpret_cast<const float4*>(scale + c) : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
     ss += v[j].x * v[j].x + v[j].y * v[j].y + v[j].z * v[j].z + v[j].w * v[j].w;
   }
   ss = rows_sum(lane_sum16(ss));
@@ -66,7 +68,7 @@ __global__ __launch_bounds__(256) void k_rmsnorm_reg(const float* x, const float
   for (int j = 0; j < 4; ++j) {
     const int c = lane * 4 + j * 256;
     if (c < dim) {
-      const float4 s = *reinterpret_cast<const float4*>(scale + c);
+      const float4 s = g[j];
       const half4 h = {(_Float16)((v[j].x / denom) * s.x), (_Float16)((v[j].y / denom) * s.y),
                        (_Float16)((v[j].z / denom) * s.z), (_Float16)((v[j].w / denom) * s.w)};
       *reinterpret_cast<half4*>(dst + c) = h;
