@@ -327,7 +327,7 @@ def main():
     world = int(os.environ.get("WORLD_SIZE", "1"))
     if args.gpus != 1 or world != 1:
         print("bench.py measures one GPU only: this build runs the whole forecast on a single MI355X "
-              "(series shard across GPUs with no collectives; see DESIGN.md). Use --gpus 1.", file=sys.stderr)
+              "(series would shard across GPUs with no collectives). Use --gpus 1.", file=sys.stderr)
         sys.exit(2)
 
     import torch
