@@ -60,3 +60,18 @@ def test_no_cpu_fallback_in_product():
             if f.endswith((".py", ".cpp", ".hip", ".h")):
                 text = open(os.path.join(dirpath, f), errors="ignore").read()
                 assert "t0ref" not in text and "libt0ref" not in text, f
+
+
+def test_bench_refuses_more_than_one_gpu():
+    """bench.py measures one GPU: --gpus N > 1 (or a multi-rank launch) exits with status 2 and says
+    so, before it touches torch or the GPU."""
+    import subprocess
+    import sys
+    for args, env in ((["--gpus", "2"], {}), ([], {"WORLD_SIZE": "2"})):
+        r = subprocess.run([sys.executable, os.path.join(ROOT, "bench.py"), *args], capture_output=True, text=True,
+                           env={**os.environ, **env}, timeout=60)
+        assert r.returncode == 2, r.stderr
+        assert "one GPU only" in r.stderr and r.stdout == ""
+    r = subprocess.run([sys.executable, os.path.join(ROOT, "bench.py"), "--steps", "0"], capture_output=True, text=True,
+                       timeout=60)
+    assert r.returncode == 2 and "at least 1" in r.stderr
