@@ -129,6 +129,15 @@ int t0h_model_profile_kind(t0h_model* model, const char* kind);
 int t0h_model_profile_entry(t0h_model* model, size_t i, char* name, size_t name_cap, uint64_t* launches,
                             double* total_ms);
 
+/* Replay of the window forward as a HIP graph (no counterpart in the reference,
+ * whose one-encoder, one-submit forward (t0-fast model.rs:693-808) is the
+ * WebGPU analogue).  On by default: each forecast window's ~95 kernel launches
+ * run eagerly the first time a window shape, input/output pointer pair and
+ * workspace state is seen, are captured on the second and replayed after
+ * that; off (enable = 0) every window runs eagerly.  Results are identical
+ * either way.  While the profiler records events, windows run eagerly. */
+int t0h_model_graph_replay(t0h_model* model, int enable);
+
 /* ---- forward ----------------------------------------------------------- */
 /* ≡ model::forward_async (t0-fast model.rs:693-808) ≡ T0Model::forward (t0-core
  * model.rs:159-244): `series` already padded to whole patches and scaled.

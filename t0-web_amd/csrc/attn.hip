@@ -487,6 +487,13 @@ void check_common(const AttnDesc& d) {
     throw Error(T0H_ERR_UNSUPPORTED, "attention: head_dim must be 64 (embed_dim = 64 * num_heads)");
 }
 
+template <int MAXKT>
+void run_time_attn(const AttnDesc& d, size_t lds, hipStream_t s) {
+  static std::atomic<uint64_t> lds_set{0};  // per instantiation
+  allow_dynamic_lds(reinterpret_cast<const void*>(&k_time_attn<MAXKT>), lds_set);
+  hipLaunchKernelGGL(k_time_attn<MAXKT>, dim3(d.v * d.heads), dim3(TA_WAVES * 64), lds, s, d);
+}
+
 }  // namespace
 
 void launch_time_attention(const AttnDesc& d, hipStream_t s) {
@@ -499,20 +506,14 @@ void launch_time_attention(const AttnDesc& d, hipStream_t s) {
   static_assert(T0H_MAX_PATCHES <= 16 * 16, "the largest instance covers 16 key tiles of 16");
   const size_t lds = time_attn_lds(d.p);
   const int kt = round_up(d.p, 32) / 16;
-  auto go = [&](auto kern) {
-    check_hip(hipFuncSetAttribute(reinterpret_cast<const void*>(kern), hipFuncAttributeMaxDynamicSharedMemorySize,
-                                  (int)lds),
-              "hipFuncSetAttribute(k_time_attn)");
-    hipLaunchKernelGGL(kern, dim3(d.v * d.heads), dim3(TA_WAVES * 64), lds, s, d);
-  };
   if (kt <= 4)
-    go(&k_time_attn<4>);
+    run_time_attn<4>(d, lds, s);
   else if (kt <= 8)
-    go(&k_time_attn<8>);
+    run_time_attn<8>(d, lds, s);
   else if (kt <= 12)
-    go(&k_time_attn<12>);
+    run_time_attn<12>(d, lds, s);
   else
-    go(&k_time_attn<16>);
+    run_time_attn<16>(d, lds, s);
   check_hip(hipGetLastError(), "k_time_attn launch");
 }
 

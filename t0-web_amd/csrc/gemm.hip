@@ -1689,13 +1689,8 @@ void run_gemm(const GemmDesc& d, hipStream_t s) {
   const int hb = EPI == EPI_SWIGLU_F16 ? C::BN / 2 : C::BN;
   const int tiles_n = (d.N + hb - 1) / hb;
   const int tiles_m = (d.M + C::BM - 1) / C::BM;
-  static bool attr_set = false;  // per instantiation
-  if (!attr_set) {
-    check_hip(hipFuncSetAttribute(reinterpret_cast<const void*>(&k_gemm<WT, A32, EPI, K64, TI, TJ>),
-                                  hipFuncAttributeMaxDynamicSharedMemorySize, C::LDS),
-              "hipFuncSetAttribute(k_gemm)");
-    attr_set = true;
-  }
+  static std::atomic<uint64_t> lds_set{0};  // per instantiation
+  allow_dynamic_lds(reinterpret_cast<const void*>(&k_gemm<WT, A32, EPI, K64, TI, TJ>), lds_set);
   hipLaunchKernelGGL((k_gemm<WT, A32, EPI, K64, TI, TJ>), dim3(tiles_m * tiles_n), dim3(256), C::LDS, s, d);
   check_hip(hipGetLastError(), "k_gemm launch");
 }
@@ -1712,13 +1707,8 @@ void run_gemm_dma(const GemmDesc& d, hipStream_t s) {
   const int hb = EPI == EPI_SWIGLU_F16 ? DM_BN / 2 : DM_BN;
   const int tiles_n = (d.N + hb - 1) / hb;
   const int tiles_m = (d.M + DM_BM - 1) / DM_BM;
-  static bool attr_set = false;
-  if (!attr_set) {
-    check_hip(hipFuncSetAttribute(reinterpret_cast<const void*>(&k_gemm_dma<WT, EPI>),
-                                  hipFuncAttributeMaxDynamicSharedMemorySize, DM_LDS),
-              "hipFuncSetAttribute(k_gemm_dma)");
-    attr_set = true;
-  }
+  static std::atomic<uint64_t> lds_set{0};  // per instantiation
+  allow_dynamic_lds(reinterpret_cast<const void*>(&k_gemm_dma<WT, EPI>), lds_set);
   hipLaunchKernelGGL((k_gemm_dma<WT, EPI>), dim3(tiles_m * tiles_n), dim3(256), DM_LDS, s, d);
   check_hip(hipGetLastError(), "k_gemm_dma launch");
 }
@@ -1728,13 +1718,8 @@ void run_gemm_bf(const GemmDesc& d, hipStream_t s) {
   using C = BfCfg<NWV>;
   const int hb = EPI == EPI_SWIGLU_F16 ? C::BN / 2 : C::BN;
   const int n_tiles = ((d.N + hb - 1) / hb) * ((d.M + BF_BM - 1) / BF_BM);
-  static bool attr_set = false;  // per instantiation
-  if (!attr_set) {
-    check_hip(hipFuncSetAttribute(reinterpret_cast<const void*>(&k_gemm_bf<WT, EPI, NWV, A32>),
-                                  hipFuncAttributeMaxDynamicSharedMemorySize, C::LDS),
-              "hipFuncSetAttribute(k_gemm_bf)");
-    attr_set = true;
-  }
+  static std::atomic<uint64_t> lds_set{0};  // per instantiation
+  allow_dynamic_lds(reinterpret_cast<const void*>(&k_gemm_bf<WT, EPI, NWV, A32>), lds_set);
   hipLaunchKernelGGL((k_gemm_bf<WT, EPI, NWV, A32>), dim3(n_tiles), dim3(64 * NWV), C::LDS, s, d);
   check_hip(hipGetLastError(), "k_gemm_bf launch");
 }
@@ -1776,9 +1761,8 @@ void run_gemv(const GemmDesc& d, hipStream_t s) {
   const int seg_rows = EPI == EPI_SWIGLU_F16 ? GV_NR / 2 : GV_NR;
   const int gx = (d.N + seg_rows - 1) / seg_rows, gy = (d.M + MT - 1) / MT;
   if (lds > 160 * 1024) throw Error(T0H_ERR_UNSUPPORTED, "gemv: K too large for the LDS row stage");
-  check_hip(hipFuncSetAttribute(reinterpret_cast<const void*>(&k_gemv<WT, A32, EPI, MT>),
-                                hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds),
-            "hipFuncSetAttribute(k_gemv)");
+  static std::atomic<uint64_t> lds_set{0};  // per instantiation
+  allow_dynamic_lds(reinterpret_cast<const void*>(&k_gemv<WT, A32, EPI, MT>), lds_set);
   hipLaunchKernelGGL((k_gemv<WT, A32, EPI, MT>), dim3(gx, gy), dim3(256), lds, s, d);
   check_hip(hipGetLastError(), "k_gemv launch");
 }
@@ -1787,9 +1771,8 @@ template <int WT, bool A32, int EPI, int MT, int NP>
 void run_gemv_s(const GemmDesc& d, hipStream_t s) {
   const size_t lds = (size_t)MT * GS_XS * sizeof(float);
   const int per = EPI == EPI_SWIGLU_F16 ? GS_NR / 2 : GS_NR;
-  check_hip(hipFuncSetAttribute(reinterpret_cast<const void*>(&k_gemv_s<WT, A32, EPI, MT, NP>),
-                                hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds),
-            "hipFuncSetAttribute(k_gemv_s)");
+  static std::atomic<uint64_t> lds_set{0};  // per instantiation
+  allow_dynamic_lds(reinterpret_cast<const void*>(&k_gemv_s<WT, A32, EPI, MT, NP>), lds_set);
   hipLaunchKernelGGL((k_gemv_s<WT, A32, EPI, MT, NP>), dim3((d.N + per - 1) / per), dim3(256), lds, s, d);
   check_hip(hipGetLastError(), "k_gemv_s launch");
 }
@@ -1832,9 +1815,8 @@ void run_gemm_mid(const GemmDesc& d, hipStream_t s) {
   const int W = EPI == EPI_SWIGLU_F16 ? 16 : 32 * TJ;
   const size_t lds = (size_t)nw * TI * TJ * 16 * 64 * 4 + (size_t)TI * 32 * (W + 4) * 4;
   const int strips = (d.N + W - 1) / W, mt = (d.M + 32 * TI - 1) / (32 * TI);
-  check_hip(hipFuncSetAttribute(reinterpret_cast<const void*>(&k_gemm_mid<WT, A32, EPI, TI, KR, TJ>),
-                                hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds),
-            "hipFuncSetAttribute(k_gemm_mid)");
+  static std::atomic<uint64_t> lds_set{0};  // per instantiation
+  allow_dynamic_lds(reinterpret_cast<const void*>(&k_gemm_mid<WT, A32, EPI, TI, KR, TJ>), lds_set);
   hipLaunchKernelGGL((k_gemm_mid<WT, A32, EPI, TI, KR, TJ>), dim3(strips * mt), dim3(64 * nw), lds, s, d);
   check_hip(hipGetLastError(), "k_gemm_mid launch");
 }

@@ -5,10 +5,17 @@
 
 #include <hip/hip_runtime.h>
 
+#include <atomic>
 #include <cstddef>
 #include <cstdint>
 
 namespace t0h {
+
+// Raises kernel `fn`'s dynamic-LDS limit to everything the CU's 160 KB leaves
+// after its static LDS, once per device: `done` holds one bit per device id
+// (a static per kernel instantiation).  Launches still request only what they
+// use; no launch calls hipFuncSetAttribute after the first one on a device.
+void allow_dynamic_lds(const void* fn, std::atomic<uint64_t>& done);
 
 // ---- quantized / f16 GEMM --------------------------------------------------
 enum Epilogue {

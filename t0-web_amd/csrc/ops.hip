@@ -357,6 +357,18 @@ unsigned blocks(long long n, int per) { return (unsigned)((n + per - 1) / per); 
 
 }  // namespace
 
+void allow_dynamic_lds(const void* fn, std::atomic<uint64_t>& done) {
+  int dev = 0;
+  check_hip(hipGetDevice(&dev), "hipGetDevice");
+  const uint64_t bit = 1ull << (dev & 63);
+  if (done.load(std::memory_order_acquire) & bit) return;
+  hipFuncAttributes fa;
+  check_hip(hipFuncGetAttributes(&fa, fn), "hipFuncGetAttributes");
+  const int cap = 160 * 1024 - (int)fa.sharedSizeBytes;
+  check_hip(hipFuncSetAttribute(fn, hipFuncAttributeMaxDynamicSharedMemorySize, cap), "hipFuncSetAttribute");
+  done.fetch_or(bit, std::memory_order_release);
+}
+
 void launch_rmsnorm(const float* x, const float* scale, _Float16* out, const int* row_map, int rows, int dim,
                     hipStream_t s) {
   if (rows <= 0) return;
@@ -377,9 +389,8 @@ void launch_window_prep(const WindowDesc& w, const PatchOut& o, hipStream_t s) {
     throw Error(T0H_ERR_INVALID_ARG, "prep: null output arrays");
   const size_t lds = prep_lds(w.t, w.ps);
   if (lds > 160 * 1024) throw Error(T0H_ERR_UNSUPPORTED, "prep: window too long for one workgroup");
-  check_hip(hipFuncSetAttribute(reinterpret_cast<const void*>(&k_prep_rows), hipFuncAttributeMaxDynamicSharedMemorySize,
-                                (int)lds),
-            "hipFuncSetAttribute(k_prep_rows)");
+  static std::atomic<uint64_t> lds_set{0};
+  allow_dynamic_lds(reinterpret_cast<const void*>(&k_prep_rows), lds_set);
   hipLaunchKernelGGL(k_prep_rows, dim3(w.v), dim3(256), lds, s, w, o);
   check_hip(hipGetLastError(), "k_prep_rows launch");
 }

@@ -69,12 +69,39 @@ struct Stage {
   bool pending = false;
 };
 
+// A window forward captured as a HIP graph.  It is replayed only while every
+// value the captured launches bake in is unchanged: the window shape, the
+// longest group segment (which picks the group-attention kernel), the input
+// and output pointers and the workspace generation (the allocation count, so
+// that a buffer reallocated since the capture is never replayed).
+struct GraphKey {
+  int v = 0, t_ctx = 0, horizon = 0, seg_max = 0;
+  const void* ctx = nullptr;
+  const void* out = nullptr;
+  uint64_t ws_gen = 0;
+  bool operator==(const GraphKey& o) const {
+    return v == o.v && t_ctx == o.t_ctx && horizon == o.horizon && seg_max == o.seg_max && ctx == o.ctx &&
+           out == o.out && ws_gen == o.ws_gen;
+  }
+};
+struct GraphEntry {
+  GraphKey key;
+  hipGraphExec_t exec = nullptr;  // null: seen once, run eagerly
+  uint64_t last_use = 0;
+};
+
 struct Workspace {
   std::unordered_map<std::string, Buf> bufs;
   std::unordered_map<std::string, Stage> stages;
+  // last bytes uploaded by put_cached per buffer (skipped when unchanged)
+  std::unordered_map<std::string, std::vector<uint8_t>> shadow;
   uint64_t allocs = 0;
   int rope_p = -1;
   int seg_max = 0;  // longest group segment of the last upload_segments
+  bool capturing = false;  // a graph capture is recording this model's launches
+  bool graphs = true;      // window forwards are captured and replayed
+  std::vector<GraphEntry> graph_cache;
+  uint64_t graph_clock = 0;
 };
 
 // Per-kernel-kind timing with HIP events recorded on the model's stream around
@@ -124,6 +151,8 @@ T* ws_get(t0h_model* m, const char* name, size_t count) {
   Buf& b = m->ws.bufs[name];
   const size_t bytes = std::max<size_t>(count * sizeof(T), 256);
   if (b.cap < bytes) {
+    if (m->ws.capturing)
+      throw Error(T0H_ERR_HIP, std::string("internal: workspace buffer ") + name + " grew during graph capture");
     if (b.p) {
       hip_check(hipStreamSynchronize(m->stream), "hipStreamSynchronize");
       hip_check(hipFree(b.p), "hipFree");
@@ -171,6 +200,26 @@ T* put(t0h_model* m, const char* name, const T* src, size_t n) {
   st.pending = true;
   return dst;
 }
+// put() for small metadata arrays that often repeat call to call: skipped when
+// the bytes equal the last ones this buffer received through put_cached and
+// the buffer has not been reallocated since (nothing else writes these buffers).
+template <typename T>
+const T* put_cached(t0h_model* m, const char* name, const T* src, size_t n) {
+  const size_t bytes = n * sizeof(T);
+  const uint64_t gen = m->ws.allocs;
+  T* dst = ws_get<T>(m, name, n);
+  std::vector<uint8_t>& sh = m->ws.shadow[name];
+  const bool same = gen == m->ws.allocs && sh.size() == bytes + sizeof(void*) &&
+                    std::memcmp(sh.data(), &dst, sizeof(void*)) == 0 &&
+                    (bytes == 0 || std::memcmp(sh.data() + sizeof(void*), src, bytes) == 0);
+  if (same) return dst;
+  put(m, name, src, n);
+  sh.resize(bytes + sizeof(void*));
+  std::memcpy(sh.data(), &dst, sizeof(void*));
+  if (bytes) std::memcpy(sh.data() + sizeof(void*), src, bytes);
+  return dst;
+}
+
 template <typename T>
 void download(t0h_model* m, T* dst, const T* src, size_t n) {
   if (n) hip_check(hipMemcpyAsync(dst, src, n * sizeof(T), hipMemcpyDeviceToHost, m->stream), "hipMemcpyAsync D2H");
@@ -415,9 +464,9 @@ void upload_segments(t0h_model* m, const std::vector<int64_t>& row_group, bool c
     std::fill(begin.begin(), begin.end(), 0);
     std::fill(len.begin(), len.end(), v);
   }
-  put(m, "perm", perm.data(), v);
-  put(m, "seg_begin", begin.data(), v);
-  put(m, "seg_len", len.data(), v);
+  put_cached(m, "perm", perm.data(), v);
+  put_cached(m, "seg_begin", begin.data(), v);
+  put_cached(m, "seg_len", len.data(), v);
   m->ws.seg_max = v ? *std::max_element(len.begin(), len.end()) : 0;
 }
 
@@ -492,8 +541,8 @@ PatchMeta patch_buffers(t0h_model* m, int v, int p) {
 }
 
 // Patch encoder + transformer layers (t0-fast model.rs:727-786 ≡ t0-core model.rs:184-229).
-// Expects enc_in / patch metadata / segments in the workspace.  Leaves the f32
-// residual stream in "x".
+// Expects enc_in / patch metadata / segments and the RoPE tables of p patches
+// (ensure_rope) in the workspace.  Leaves the f32 residual stream in "x".
 void encode_and_layers(t0h_model* m, int v, int p, const PatchMeta& pm, float* trace_pe, float* trace_l0) {
   const t0h_config& c = m->mc.c;
   const int E = (int)c.embed_dim, ps = (int)c.patch_size, M = v * p;
@@ -507,7 +556,7 @@ void encode_and_layers(t0h_model* m, int v, int p, const PatchMeta& pm, float* t
   const int* perm = ws_get<int>(m, "perm", v);
   const int* seg_begin = ws_get<int>(m, "seg_begin", v);
   const int* seg_len = ws_get<int>(m, "seg_len", v);
-  ensure_rope(m, p);
+  if (m->ws.rope_p != p) throw Error(T0H_ERR_HIP, "internal: RoPE tables not prepared for this window");
 
   // patch encoder residual block + type embedding (model.rs:199-207)
   {
@@ -594,6 +643,85 @@ float* decode_rows(t0h_model* m, int rows, const int* map) {
   return dout;
 }
 
+// Grows every buffer encode_and_layers and decode_rows use for `rows` patch
+// rows and `dec_rows` decoded rows, so that neither allocates once launches start.
+void reserve_forward(t0h_model* m, int rows, int dec_rows) {
+  const t0h_config& c = m->mc.c;
+  const size_t M = (size_t)rows, E = c.embed_dim, wide = std::max<size_t>(E, (size_t)m->enc.hid.n);
+  ws_get<float>(m, "x", M * E);
+  ws_get<_Float16>(m, "xn", M * wide);
+  ws_get<_Float16>(m, "qkv", M * 3 * E);
+  ws_get<_Float16>(m, "h", M * c.mlp_hidden_dim);
+  ws_get<_Float16>(m, "dec_in", (size_t)dec_rows * E);
+  ws_get<_Float16>(m, "dec_h", (size_t)dec_rows * m->dec.hid.n);
+  ws_get<float>(m, "dec_out", (size_t)dec_rows * m->dec.out.n);
+}
+
+void destroy_graphs(t0h_model* m) {
+  for (GraphEntry& e : m->ws.graph_cache)
+    if (e.exec) (void)hipGraphExecDestroy(e.exec);
+  m->ws.graph_cache.clear();
+}
+
+// Runs `launches` on the model's stream.  The first call with a key runs them
+// eagerly, the second captures them into a HIP graph and launches it, later
+// ones replay the graph.  Eager always while the profiler records events or
+// replay is switched off.  At most kGraphs graphs are kept (least recently
+// used evicted); entries of an older workspace generation are dropped.
+template <typename F>
+void run_graphed(t0h_model* m, const GraphKey& key, F&& launches) {
+  constexpr size_t kGraphs = 8;
+  Workspace& ws = m->ws;
+  if (!ws.graphs || m->prof.on) {
+    launches();
+    return;
+  }
+  auto& cache = ws.graph_cache;
+  // a graph may still be executing: the stream drains before one is destroyed
+  auto drop = [&](std::vector<GraphEntry>::iterator it) {
+    if (it->exec) {
+      sync(m);
+      (void)hipGraphExecDestroy(it->exec);
+    }
+    return cache.erase(it);
+  };
+  for (auto it = cache.begin(); it != cache.end();) it = it->key.ws_gen != key.ws_gen ? drop(it) : it + 1;
+  GraphEntry* e = nullptr;
+  for (GraphEntry& g : cache)
+    if (g.key == key) e = &g;
+  if (!e) {
+    launches();
+    if (cache.size() >= kGraphs) {
+      drop(std::min_element(cache.begin(), cache.end(),
+                            [](const GraphEntry& a, const GraphEntry& b) { return a.last_use < b.last_use; }));
+    }
+    cache.push_back(GraphEntry{key, nullptr, ++ws.graph_clock});
+    return;
+  }
+  e->last_use = ++ws.graph_clock;
+  if (!e->exec) {
+    hip_check(hipStreamBeginCapture(m->stream, hipStreamCaptureModeThreadLocal), "hipStreamBeginCapture");
+    ws.capturing = true;
+    hipGraph_t g = nullptr;
+    try {
+      launches();
+    } catch (...) {
+      ws.capturing = false;
+      if (hipStreamEndCapture(m->stream, &g) == hipSuccess && g) (void)hipGraphDestroy(g);
+      (void)hipGetLastError();
+      throw;
+    }
+    ws.capturing = false;
+    hip_check(hipStreamEndCapture(m->stream, &g), "hipStreamEndCapture");
+    hipGraphExec_t exec = nullptr;
+    const hipError_t rc = hipGraphInstantiate(&exec, g, nullptr, nullptr, 0);
+    (void)hipGraphDestroy(g);
+    hip_check(rc, "hipGraphInstantiate");
+    e->exec = exec;
+  }
+  hip_check(hipGraphLaunch(e->exec, m->stream), "hipGraphLaunch");
+}
+
 // ---- forecast window (lib.rs:50-97) on device ----
 struct WindowRows {
   int t_ctx = 0, horizon = 0;
@@ -629,10 +757,11 @@ void forecast_window(t0h_model* m, const WindowRows& wr, float* d_out) {
     dense[r] = (int)(std::lower_bound(sorted.begin(), sorted.end(), wr.group[r]) - sorted.begin());
     dense64[r] = dense[r];
   }
-  const int64_t* d_off = put(m, "win_off", wr.src_off.data(), v);
-  const int* d_len = put(m, "win_len", wr.len.data(), v);
-  const int* d_grp = put(m, "win_grp", dense.data(), v);
+  const int64_t* d_off = put_cached(m, "win_off", wr.src_off.data(), v);
+  const int* d_len = put_cached(m, "win_len", wr.len.data(), v);
+  const int* d_grp = put_cached(m, "win_grp", dense.data(), v);
   upload_segments(m, dense64, true);
+  ensure_rope(m, p);
 
   WindowDesc w;
   w.ctx = wr.d_ctx;
@@ -648,32 +777,45 @@ void forecast_window(t0h_model* m, const WindowRows& wr, float* d_out) {
   w.use_arcsinh = c.scaler_use_arcsinh;
   w.variance_offset = c.scaler_variance_offset;
   w.eps = c.scaler_eps;
-  PatchMeta pm = patch_buffers(m, v, p);
-  {
-    ProfScope ps_(m, "prep");
-    PatchOut po{pm.enc_in, pm.grp, pm.att, pm.type_idx, pm.type_raw, pm.fut, pm.patch_loc, pm.patch_scale};
-    launch_window_prep(w, po, s);
-  }
-  encode_and_layers(m, v, p, pm, nullptr, nullptr);
-  if (hp == 0) return;
-  int* map = ws_get<int>(m, "dec_map", (size_t)v * hp);
-  launch_gather_map(map, v, p, ctx_p, hp, s);
-  float* dout = decode_rows(m, v * hp, map);
-  ProfScope ps_(m, "forecast_out");
-  ForecastOutDesc od;
-  od.dec = dout;
-  od.patch_loc = pm.patch_loc;
-  od.patch_scale = pm.patch_scale;
-  od.out = d_out;
-  od.v = v;
-  od.p = p;
-  od.ctx_p = ctx_p;
-  od.hp = hp;
-  od.ps = ps;
-  od.nq = nq;
-  od.horizon = wr.horizon;
-  od.use_arcsinh = c.scaler_use_arcsinh;
-  launch_forecast_out(od, s);
+  const PatchMeta pm = patch_buffers(m, v, p);
+  reserve_forward(m, v * p, v * std::max(hp, 1));
+  int* map = ws_get<int>(m, "dec_map", (size_t)v * std::max(hp, 1));
+
+  auto launches = [&]() {
+    {
+      ProfScope ps_(m, "prep");
+      PatchOut po{pm.enc_in, pm.grp, pm.att, pm.type_idx, pm.type_raw, pm.fut, pm.patch_loc, pm.patch_scale};
+      launch_window_prep(w, po, s);
+    }
+    encode_and_layers(m, v, p, pm, nullptr, nullptr);
+    if (hp == 0) return;
+    launch_gather_map(map, v, p, ctx_p, hp, s);
+    float* dout = decode_rows(m, v * hp, map);
+    ProfScope ps_(m, "forecast_out");
+    ForecastOutDesc od;
+    od.dec = dout;
+    od.patch_loc = pm.patch_loc;
+    od.patch_scale = pm.patch_scale;
+    od.out = d_out;
+    od.v = v;
+    od.p = p;
+    od.ctx_p = ctx_p;
+    od.hp = hp;
+    od.ps = ps;
+    od.nq = nq;
+    od.horizon = wr.horizon;
+    od.use_arcsinh = c.scaler_use_arcsinh;
+    launch_forecast_out(od, s);
+  };
+  GraphKey key;
+  key.v = v;
+  key.t_ctx = wr.t_ctx;
+  key.horizon = wr.horizon;
+  key.seg_max = m->ws.seg_max;
+  key.ctx = wr.d_ctx;
+  key.out = d_out;
+  key.ws_gen = m->ws.allocs;
+  run_graphed(m, key, launches);
 }
 
 void require(bool ok, const char* msg) {
@@ -887,6 +1029,7 @@ void t0h_model_destroy(t0h_model* m) {
   if (!m) return;
   (void)hipSetDevice(m->ctx->device);
   (void)hipStreamSynchronize(m->stream);
+  destroy_graphs(m);
   for (auto& kv : m->ws.bufs)
     if (kv.second.p) (void)hipFree(kv.second.p);
   for (auto& kv : m->ws.stages) {
@@ -977,6 +1120,18 @@ int t0h_model_profile_entry(t0h_model* m, size_t i, char* name, size_t name_cap,
   API_END
 }
 
+int t0h_model_graph_replay(t0h_model* m, int enable) {
+  API_BEGIN
+  require(m != nullptr, "t0h_model_graph_replay: NULL model");
+  bind_device(m);
+  if (!enable) {
+    sync(m);
+    destroy_graphs(m);
+  }
+  m->ws.graphs = enable != 0;
+  API_END
+}
+
 int t0h_forward(t0h_model* m, const t0h_series* sr, float* out, size_t out_len, float* trace_pe, float* trace_l0) {
   API_BEGIN
   require(m && sr && out, "t0h_forward: NULL argument");
@@ -1021,6 +1176,7 @@ int t0h_forward(t0h_model* m, const t0h_series* sr, float* out, size_t out_len, 
   PatchOut po{pm.enc_in, pm.grp, pm.att, pm.type_idx, pm.type_raw, pm.fut, nullptr, nullptr};
   launch_series_patchify(sd, po, m->stream);
   launch_fut_rows(pm.type_raw, pm.fut, v, p, m->stream);
+  ensure_rope(m, p);
   encode_and_layers(m, v, p, pm, trace_pe, trace_l0);
   const int M = v * p;
   float* dout = decode_rows(m, M, nullptr);

@@ -73,7 +73,7 @@ _lib = None
 SYMBOLS = [
     "t0h_last_error", "t0h_abi_version", "t0h_ctx_create", "t0h_ctx_destroy", "t0h_gguf_inspect",
     "t0h_model_load_gguf", "t0h_model_destroy", "t0h_model_config", "t0h_model_weight_bytes", "t0h_model_stream",
-    "t0h_model_workspace", "t0h_model_profile", "t0h_model_profile_kind", "t0h_model_profile_entry", "t0h_forward", "t0h_forecast", "t0h_forecast_batch_chunked",
+    "t0h_model_workspace", "t0h_model_profile", "t0h_model_profile_kind", "t0h_model_profile_entry", "t0h_model_graph_replay", "t0h_forward", "t0h_forecast", "t0h_forecast_batch_chunked",
     "t0h_forecast_batch_rows_chunked", "t0h_forecast_grouped", "t0h_forecast_grouped_dev",
     "t0h_forecast_grouped_ar", "t0h_forecast_rollout", "t0h_dequant", "t0h_gemm_q", "t0h_gemm_f16", "t0h_row_bytes",
     "t0h_quantize", "t0h_synth_model_gguf", "t0h_export_gguf",
@@ -107,6 +107,7 @@ def lib():
     L.t0h_model_profile.argtypes = [P, I]
     L.t0h_model_profile_kind.argtypes = [P, C.c_char_p]
     L.t0h_model_profile_entry.argtypes = [P, S, C.c_char_p, S, C.POINTER(C.c_uint64), C.POINTER(C.c_double)]
+    L.t0h_model_graph_replay.argtypes = [P, I]
     L.t0h_forward.argtypes = [P, C.POINTER(Series), P, S, P, P]
     L.t0h_forecast.argtypes = [P, P, S, S, S, P, S]
     L.t0h_forecast_batch_chunked.argtypes = [P, P, S, S, S, S, P, S]
@@ -284,6 +285,10 @@ class GpuModel:
             out[name.value.decode()] = (n.value, ms.value)
             i += 1
         return out
+
+    def graph_replay(self, enable=True):
+        """Capture and replay each window forward as a HIP graph (default) or run it eagerly."""
+        _check(lib().t0h_model_graph_replay(self.h, int(enable)))
 
     def workspace(self):
         r, a = C.c_uint64(), C.c_uint64()

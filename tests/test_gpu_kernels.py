@@ -96,18 +96,34 @@ def test_gemm_sweep(torch_cuda, t0hip, oracle, rng, qtype, k, n, m):
 
 
 @pytest.mark.parametrize("qtype", [8, 2])
-def test_gemm_config1_and_m8192(torch_cuda, t0hip, oracle, rng, qtype):
-    """BASELINE config 1 (M=512, K=768, N=2304) and the M=8192 end of the sweep (row sample)."""
-    k, n = 768, 2304
+def test_gemm_config1(torch_cuda, t0hip, oracle, rng, qtype):
+    """M=512, K=768, N=2304, every row."""
+    k, n, m = 768, 2304, 512
     W = (0.02 * rng.standard_normal((n, k))).astype(np.float32)
     blocks = oracle.quantize(qtype, W)
     deq = oracle.dequantize(qtype, blocks, n * k).reshape(n, k).astype(np.float64)
-    for m in (512, 8192):
-        x = rng.standard_normal((m, k)).astype(np.float32)
-        got = run_gemm(torch_cuda, t0hip, qtype, blocks, x, None, n)
-        rows = np.arange(m) if m <= 512 else rng.choice(m, 512, replace=False)
-        want = x[rows].astype(np.float64) @ deq.T
-        assert rel_err(got[rows], want) < 1e-2
+    x = rng.standard_normal((m, k)).astype(np.float32)
+    got = run_gemm(torch_cuda, t0hip, qtype, blocks, x, None, n)
+    assert rel_err(got, x.astype(np.float64) @ deq.T) < 1e-2
+
+
+@pytest.mark.parametrize("qtype", [8, 2])
+@pytest.mark.parametrize("k,n", SHAPES)
+def test_gemm_m8192(torch_cuda, t0hip, oracle, rng, qtype, k, n):
+    """The M=8192 end of the config-2 sweep at every (K, N) the bench reports (the f32-activation
+    256x256 register-operand kernel, K = 2048 included): 512 sampled rows plus the first and last
+    256-row tile against float64, bias on."""
+    m = 8192
+    W = (0.02 * rng.standard_normal((n, k))).astype(np.float32)
+    b = (0.02 * rng.standard_normal(n)).astype(np.float32)
+    blocks = oracle.quantize(qtype, W)
+    deq = oracle.dequantize(qtype, blocks, n * k).reshape(n, k).astype(np.float64)
+    x = rng.standard_normal((m, k)).astype(np.float32)
+    got = run_gemm(torch_cuda, t0hip, qtype, blocks, x, b, n)
+    rows = np.unique(np.concatenate([np.arange(256), np.arange(m - 256, m), rng.choice(m, 512, replace=False)]))
+    want = x[rows].astype(np.float64) @ deq.T + b
+    assert np.isfinite(got).all()
+    assert rel_err(got[rows], want) < 1e-2
 
 
 @pytest.mark.parametrize("m", [1, 3, 40, 200])

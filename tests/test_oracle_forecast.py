@@ -109,3 +109,21 @@ def test_causal_stats_closed_form_matches_oracle_scaler(oracle):
         wl, ws = np_ref.causal_stats(x.astype(np.float64), mask, g, eps, offset)
         assert np.max(np.abs(loc - wl)) < 2e-4
         assert np.max(np.abs(scale - ws) / ws) < 1e-4
+
+
+def test_rollout_driver_reproduces_oracle_rollout(tiny, oracle):
+    """tests/util.py's rollout driver (lib.rs:259-341 in Python, reused by the GPU tests to feed
+    both paths the same windows) reproduces the oracle's forecast_rollout bit for bit, on the
+    reference's long-rollout fixture context (ctx 4096, horizon 1200: one 1024-step block, then the
+    saturating 192-step block over 134 patches)."""
+    import os
+    from util import rollout_blocks
+    om, T, c = tiny
+    ctx = np.fromfile(os.path.join(os.path.dirname(__file__), "golden", "case_long_rollout_context.f32"), "<f4")
+    q = np.array([0.1, 0.25, 0.5, 0.75, 0.9], np.float32)
+    want = om.forecast_rollout(ctx, ctx.size, 1200, q)
+    got, wins = rollout_blocks(lambda x, h: om.forecast(x[None], 1, x.size, h),
+                               lambda w, h: om.forecast_batch_chunked(w, w.shape[0], w.shape[1], h, 0),
+                               oracle, om.levels, ctx, ctx.size, 1200, q)
+    assert len(wins) == 1 and wins[0].shape == (5, 4096)
+    assert np.array_equal(got, want)
