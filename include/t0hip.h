@@ -32,6 +32,8 @@ extern "C" {
 #define T0H_MAX_QUANTILES 64
 #define T0H_MAX_HORIZON 1024 /* crates/t0-core/src/model.rs:26 MAX_HORIZON */
 #define T0H_MAX_PATCHES 256  /* time-attention window per forward, in patches */
+/* Device scratch of t0h_forecast_grouped_dev_noalloc, one per GPU (32 MiB). */
+#define T0H_NOALLOC_SCRATCH_BYTES (32u << 20)
 
 /* Status codes.  Each maps one reference failure (anyhow error or panic). */
 enum t0h_status {
@@ -169,6 +171,20 @@ int t0h_forecast_grouped(t0h_model* model, const float* contexts, const int64_t*
  * before reading d_out). */
 int t0h_forecast_grouped_dev(t0h_model* model, const float* d_contexts, const int64_t* row_group, size_t n_rows,
                              size_t t_ctx, size_t horizon, float* d_out);
+/* No counterpart in the reference: t0h_forecast_grouped_dev for callers that
+ * cannot allocate (code under HIP graph capture, tight serving loops, harnesses
+ * that forbid hipMalloc).  Same arguments and results; it calls no hipMalloc,
+ * hipHostMalloc or hipFree.  The window's workspace is carved from one static
+ * device array of T0H_NOALLOC_SCRATCH_BYTES per GPU (about 2,000 patch rows of
+ * the 768-wide model: one 2048-step series is 66 rows), and its small host
+ * metadata (group segments, RoPE tables) is staged through pinned memory the
+ * model allocated at load.  A window that needs more scratch is rejected with
+ * T0H_ERR_UNSUPPORTED before any work is issued.  Every no-allocation call on a
+ * GPU shares that GPU's scratch, which keeps the last call's contents: calls
+ * that overlap on one GPU (from different models, threads or streams) race.
+ * Enqueued on the model's stream like the _dev entry point. */
+int t0h_forecast_grouped_dev_noalloc(t0h_model* model, const float* d_contexts, const int64_t* row_group,
+                                     size_t n_rows, size_t t_ctx, size_t horizon, float* d_out);
 /* Autoregressive loop over t0h_forecast_grouped: after each step every row's
  * median-level quantile is appended and the window re-cut to the trailing
  * t_ctx values, weights staying resident.  out: [n_rows, steps*horizon, n_q]. */

@@ -17,6 +17,13 @@ namespace t0h {
 // use; no launch calls hipFuncSetAttribute after the first one on a device.
 void allow_dynamic_lds(const void* fn, std::atomic<uint64_t>& done);
 
+// The no-allocation entry point's device scratch (a static __device__ array of
+// T0H_NOALLOC_SCRATCH_BYTES): scratch_init() looks up its address on the
+// current device once (call with that device current, at context creation);
+// scratch_device_ptr(dev) returns it (throws if that device was never set up).
+void scratch_init();
+void* scratch_device_ptr(int dev);
+
 // ---- quantized / f16 GEMM --------------------------------------------------
 enum Epilogue {
   EPI_STORE_F32 = 0,  // y = acc + bias (+ row_add[row_add_idx[m]]) (relu opt.), f32 out

@@ -3,6 +3,7 @@
 // quantile head with rescale + forecast slice, and the AR window update.
 #include <hip/hip_runtime.h>
 
+#include <mutex>
 #include <string>
 
 #include "kernels.h"
@@ -356,6 +357,35 @@ __global__ __launch_bounds__(256) void k_ar_store(float* dst, const float* src, 
 unsigned blocks(long long n, int per) { return (unsigned)((n + per - 1) / per); }
 
 }  // namespace
+
+// Device scratch of the no-allocation entry point.  In host code `scratch`
+// names a host-side stand-in, never device memory: host code uses the address
+// hipGetSymbolAddress returned for the current device (g_scratch[dev]).
+static __device__ __align__(256) unsigned char scratch[T0H_NOALLOC_SCRATCH_BYTES];
+
+namespace {
+constexpr int kMaxDevices = 64;
+std::atomic<void*> g_scratch[kMaxDevices];
+std::mutex g_scratch_mu;
+}  // namespace
+
+void scratch_init() {
+  int dev = 0;
+  check_hip(hipGetDevice(&dev), "hipGetDevice");
+  if (dev < 0 || dev >= kMaxDevices) throw Error(T0H_ERR_UNSUPPORTED, "device id beyond the scratch table");
+  std::lock_guard<std::mutex> lk(g_scratch_mu);
+  if (g_scratch[dev].load(std::memory_order_acquire)) return;
+  void* ptr = nullptr;
+  check_hip(hipGetSymbolAddress(&ptr, HIP_SYMBOL(scratch)), "hipGetSymbolAddress(scratch)");
+  if (!ptr) throw Error(T0H_ERR_HIP, "hipGetSymbolAddress(scratch) returned no address");
+  g_scratch[dev].store(ptr, std::memory_order_release);
+}
+
+void* scratch_device_ptr(int dev) {
+  void* ptr = dev >= 0 && dev < kMaxDevices ? g_scratch[dev].load(std::memory_order_acquire) : nullptr;
+  if (!ptr) throw Error(T0H_ERR_INVALID_ARG, "no-allocation scratch not set up on device " + std::to_string(dev));
+  return ptr;
+}
 
 void allow_dynamic_lds(const void* fn, std::atomic<uint64_t>& done) {
   int dev = 0;

@@ -102,6 +102,17 @@ struct Workspace {
   bool graphs = true;      // window forwards are captured and replayed
   std::vector<GraphEntry> graph_cache;
   uint64_t graph_clock = 0;
+  // No-allocation mode (t0h_forecast_grouped_dev_noalloc): while `on`, every
+  // buffer is carved from the device scratch `dev` and every upload is staged
+  // through the pinned `host` region the model allocated at load.
+  struct Arena {
+    bool on = false;
+    uint8_t* dev = nullptr;
+    size_t dev_cap = 0, dev_used = 0;
+    uint8_t* host = nullptr;
+    size_t host_cap = 0, host_used = 0;
+    std::unordered_map<std::string, std::pair<void*, size_t>> named;
+  } arena;
 };
 
 // Per-kernel-kind timing with HIP events recorded on the model's stream around
@@ -140,14 +151,41 @@ struct t0h_model {
   std::vector<t0h::Layer> layers;
   t0h::Workspace ws;
   t0h::Profiler prof;
+  // pinned host staging of the no-allocation entry point (allocated at load) and
+  // the event marking when the last call's copies out of it have executed
+  void* noalloc_host = nullptr;
+  size_t noalloc_host_bytes = 0;
+  hipEvent_t noalloc_ev = nullptr;
+  bool noalloc_pending = false;
 };
 
 namespace t0h {
 namespace {
 
 // ---- workspace (grow-only, like pool.rs:75-93) ----
+// No-allocation mode: a named slice of the device scratch (256-byte aligned),
+// the same slice for every request of one name within a call.
+void* arena_get(t0h_model* m, const char* name, size_t bytes) {
+  Workspace::Arena& a = m->ws.arena;
+  auto it = a.named.find(name);
+  if (it != a.named.end()) {
+    if (it->second.second < bytes) throw Error(T0H_ERR_HIP, std::string("internal: scratch slice ") + name + " regrown");
+    return it->second.first;
+  }
+  const size_t off = (a.dev_used + 255) & ~size_t(255);
+  if (off + bytes > a.dev_cap)
+    throw Error(T0H_ERR_UNSUPPORTED, "window needs more than the " + std::to_string(a.dev_cap >> 20) +
+                                         " MiB no-allocation scratch (exhausted at buffer " + name + ", " +
+                                         std::to_string(off + bytes) + " bytes so far)");
+  a.dev_used = off + bytes;
+  void* p = a.dev + off;
+  a.named.emplace(name, std::make_pair(p, bytes));
+  return p;
+}
+
 template <typename T>
 T* ws_get(t0h_model* m, const char* name, size_t count) {
+  if (m->ws.arena.on) return static_cast<T*>(arena_get(m, name, std::max<size_t>(count * sizeof(T), 256)));
   Buf& b = m->ws.bufs[name];
   const size_t bytes = std::max<size_t>(count * sizeof(T), 256);
   if (b.cap < bytes) {
@@ -178,6 +216,16 @@ T* put(t0h_model* m, const char* name, const T* src, size_t n) {
   T* dst = ws_get<T>(m, name, n);
   if (n == 0) return dst;
   const size_t bytes = n * sizeof(T);
+  if (m->ws.arena.on) {  // staged through the pinned region allocated at load
+    Workspace::Arena& a = m->ws.arena;
+    const size_t off = (a.host_used + 63) & ~size_t(63);
+    if (off + bytes > a.host_cap)
+      throw Error(T0H_ERR_UNSUPPORTED, std::string("no-allocation host staging exhausted at ") + name);
+    a.host_used = off + bytes;
+    std::memcpy(a.host + off, src, bytes);
+    hip_check(hipMemcpyAsync(dst, a.host + off, bytes, hipMemcpyHostToDevice, m->stream), "hipMemcpyAsync H2D");
+    return dst;
+  }
   Stage& st = m->ws.stages[name];
   if (st.pending) {
     hip_check(hipEventSynchronize(st.ev), "hipEventSynchronize");
@@ -205,6 +253,7 @@ T* put(t0h_model* m, const char* name, const T* src, size_t n) {
 // the buffer has not been reallocated since (nothing else writes these buffers).
 template <typename T>
 const T* put_cached(t0h_model* m, const char* name, const T* src, size_t n) {
+  if (m->ws.arena.on) return put(m, name, src, n);  // the scratch keeps no contents of its own
   const size_t bytes = n * sizeof(T);
   const uint64_t gen = m->ws.allocs;
   T* dst = ws_get<T>(m, name, n);
@@ -478,7 +527,8 @@ void upload_segments(t0h_model* m, const std::vector<int64_t>& row_group, bool c
 // which is ops.rs:132-142 applied to ops.rs:175-181's normalized rows, with the
 // f32 table values multiplied in f64 and rounded once.
 void ensure_rope(t0h_model* m, int p) {
-  if (m->ws.rope_p == p) return;
+  const bool arena = m->ws.arena.on;  // scratch contents are not kept between calls
+  if (!arena && m->ws.rope_p == p) return;
   std::vector<float> cs, sn, sc;
   rope_tables(p, 64, cs, sn, sc);
   const size_t per = (size_t)p * 128;
@@ -498,7 +548,7 @@ void ensure_rope(t0h_model* m, int p) {
     }
   }
   put(m, "rope", t.data(), t.size());
-  m->ws.rope_p = p;
+  if (!arena) m->ws.rope_p = p;
 }
 
 GemmDesc gemm(const Mat& w, const void* a, int lda, const float* bias, void* y, int ldy, int M, int epi, int relu = 0) {
@@ -556,7 +606,7 @@ void encode_and_layers(t0h_model* m, int v, int p, const PatchMeta& pm, float* t
   const int* perm = ws_get<int>(m, "perm", v);
   const int* seg_begin = ws_get<int>(m, "seg_begin", v);
   const int* seg_len = ws_get<int>(m, "seg_len", v);
-  if (m->ws.rope_p != p) throw Error(T0H_ERR_HIP, "internal: RoPE tables not prepared for this window");
+  if (!m->ws.arena.on && m->ws.rope_p != p) throw Error(T0H_ERR_HIP, "internal: RoPE tables not prepared for this window");
 
   // patch encoder residual block + type embedding (model.rs:199-207)
   {
@@ -672,7 +722,7 @@ template <typename F>
 void run_graphed(t0h_model* m, const GraphKey& key, F&& launches) {
   constexpr size_t kGraphs = 8;
   Workspace& ws = m->ws;
-  if (!ws.graphs || m->prof.on) {
+  if (!ws.graphs || m->prof.on || ws.arena.on) {
     launches();
     return;
   }
@@ -757,6 +807,14 @@ void forecast_window(t0h_model* m, const WindowRows& wr, float* d_out) {
     dense[r] = (int)(std::lower_bound(sorted.begin(), sorted.end(), wr.group[r]) - sorted.begin());
     dense64[r] = dense[r];
   }
+  // every device buffer of the window is sized before the first upload or launch
+  const PatchMeta pm = patch_buffers(m, v, p);
+  reserve_forward(m, v * p, v * std::max(hp, 1));
+  int* map = ws_get<int>(m, "dec_map", (size_t)v * std::max(hp, 1));
+  ws_get<int64_t>(m, "win_off", v);
+  for (const char* n : {"win_len", "win_grp", "perm", "seg_begin", "seg_len"}) ws_get<int>(m, n, v);
+  ws_get<float>(m, "rope", m->layers.size() * 2 * (size_t)p * 128);
+
   const int64_t* d_off = put_cached(m, "win_off", wr.src_off.data(), v);
   const int* d_len = put_cached(m, "win_len", wr.len.data(), v);
   const int* d_grp = put_cached(m, "win_grp", dense.data(), v);
@@ -777,9 +835,6 @@ void forecast_window(t0h_model* m, const WindowRows& wr, float* d_out) {
   w.use_arcsinh = c.scaler_use_arcsinh;
   w.variance_offset = c.scaler_variance_offset;
   w.eps = c.scaler_eps;
-  const PatchMeta pm = patch_buffers(m, v, p);
-  reserve_forward(m, v * p, v * std::max(hp, 1));
-  int* map = ws_get<int>(m, "dec_map", (size_t)v * std::max(hp, 1));
 
   auto launches = [&]() {
     {
@@ -985,6 +1040,7 @@ int t0h_ctx_create(int device, t0h_ctx** out) {
   std::string arch = prop.gcnArchName;
   if (arch.rfind("gfx950", 0) != 0)
     throw Error(T0H_ERR_UNSUPPORTED, "this library is built for gfx950 (MI355X); device is " + arch);
+  scratch_init();  // this device's no-allocation scratch address, once
   auto* c = new t0h_ctx;
   c->device = device;
   c->arch = arch;
@@ -1016,7 +1072,18 @@ int t0h_model_load_gguf(t0h_ctx* ctx, const uint8_t* bytes, size_t len, t0h_mode
   hip_check(hipStreamCreateWithFlags(&m->stream, hipStreamNonBlocking), "hipStreamCreate");
   try {
     load_model(m.get(), bytes, len);
+    // pinned staging for the no-allocation entry point: RoPE tables of the longest
+    // window plus per-row metadata for as many rows as the scratch can hold
+    const size_t rows_max = T0H_NOALLOC_SCRATCH_BYTES / (4 * (size_t)m->mc.c.embed_dim);
+    m->noalloc_host_bytes = m->layers.size() * 2 * (size_t)T0H_MAX_PATCHES * 128 * 4 + 32 * rows_max + 4096;
+    if (hipHostMalloc(&m->noalloc_host, m->noalloc_host_bytes, hipHostMallocDefault) != hipSuccess) {
+      (void)hipGetLastError();
+      m->noalloc_host = nullptr;
+      throw Error(T0H_ERR_OOM, "pinned host allocation failed");
+    }
+    hip_check(hipEventCreateWithFlags(&m->noalloc_ev, hipEventDisableTiming), "hipEventCreate");
   } catch (...) {
+    if (m->noalloc_host) (void)hipHostFree(m->noalloc_host);
     if (m->d_weights) (void)hipFree(m->d_weights);
     (void)hipStreamDestroy(m->stream);
     throw;
@@ -1042,6 +1109,8 @@ void t0h_model_destroy(t0h_model* m) {
       (void)hipEventDestroy(pr.second);
     }
   for (hipEvent_t e : m->prof.spare) (void)hipEventDestroy(e);
+  if (m->noalloc_host) (void)hipHostFree(m->noalloc_host);
+  if (m->noalloc_ev) (void)hipEventDestroy(m->noalloc_ev);
   if (m->d_weights) (void)hipFree(m->d_weights);
   (void)hipStreamDestroy(m->stream);
   delete m;
@@ -1289,6 +1358,44 @@ int t0h_forecast_grouped_dev(t0h_model* m, const float* d_contexts, const int64_
   wr.horizon = (int)horizon;
   wr.d_ctx = d_contexts;
   grouped_rows(wr, row_group, n_rows, t_ctx);
+  forecast_window(m, wr, d_out);
+  API_END
+}
+
+int t0h_forecast_grouped_dev_noalloc(t0h_model* m, const float* d_contexts, const int64_t* row_group, size_t n_rows,
+                                     size_t t_ctx, size_t horizon, float* d_out) {
+  API_BEGIN
+  require(m && d_contexts && row_group && d_out, "t0h_forecast_grouped_dev_noalloc: NULL argument");
+  require(n_rows > 0 && t_ctx > 0, "t0h_forecast_grouped_dev_noalloc: n_rows and t_ctx must be positive");
+  bind_device(m);
+  WindowRows wr;
+  wr.t_ctx = (int)t_ctx;
+  wr.horizon = (int)horizon;
+  wr.d_ctx = d_contexts;
+  grouped_rows(wr, row_group, n_rows, t_ctx);
+  // the previous call's copies out of the pinned staging must have executed
+  if (m->noalloc_pending) {
+    hip_check(hipEventSynchronize(m->noalloc_ev), "hipEventSynchronize");
+    m->noalloc_pending = false;
+  }
+  Workspace::Arena& a = m->ws.arena;
+  a.on = true;
+  a.dev = static_cast<uint8_t*>(scratch_device_ptr(m->ctx->device));
+  a.dev_cap = T0H_NOALLOC_SCRATCH_BYTES;
+  a.dev_used = 0;
+  a.host = static_cast<uint8_t*>(m->noalloc_host);
+  a.host_cap = m->noalloc_host_bytes;
+  a.host_used = 0;
+  a.named.clear();
+  struct Off {  // leave no-allocation mode on every exit
+    t0h_model* m;
+    ~Off() {
+      Workspace::Arena& x = m->ws.arena;
+      if (x.host_used && hipEventRecord(m->noalloc_ev, m->stream) == hipSuccess) m->noalloc_pending = true;
+      x.on = false;
+      x.named.clear();
+    }
+  } off{m};
   forecast_window(m, wr, d_out);
   API_END
 }

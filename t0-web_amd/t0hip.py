@@ -75,6 +75,7 @@ SYMBOLS = [
     "t0h_model_load_gguf", "t0h_model_destroy", "t0h_model_config", "t0h_model_weight_bytes", "t0h_model_stream",
     "t0h_model_workspace", "t0h_model_profile", "t0h_model_profile_kind", "t0h_model_profile_entry", "t0h_model_graph_replay", "t0h_forward", "t0h_forecast", "t0h_forecast_batch_chunked",
     "t0h_forecast_batch_rows_chunked", "t0h_forecast_grouped", "t0h_forecast_grouped_dev",
+    "t0h_forecast_grouped_dev_noalloc",
     "t0h_forecast_grouped_ar", "t0h_forecast_rollout", "t0h_dequant", "t0h_gemm_q", "t0h_gemm_f16", "t0h_row_bytes",
     "t0h_quantize", "t0h_synth_model_gguf", "t0h_export_gguf",
 ]
@@ -114,6 +115,7 @@ def lib():
     L.t0h_forecast_batch_rows_chunked.argtypes = [P, P, P, S, S, S, P, S]
     L.t0h_forecast_grouped.argtypes = [P, P, P, S, S, S, P, S]
     L.t0h_forecast_grouped_dev.argtypes = [P, P, P, S, S, S, P]
+    L.t0h_forecast_grouped_dev_noalloc.argtypes = [P, P, P, S, S, S, P]
     L.t0h_forecast_grouped_ar.argtypes = [P, P, P, S, S, S, S, P, S]
     L.t0h_forecast_rollout.argtypes = [P, P, S, S, P, S, P, S]
     L.t0h_dequant.argtypes = [I, P, S, P, P]
@@ -355,6 +357,14 @@ def forecast_grouped(engine, model, contexts, row_group, t_ctx, horizon):
     out = np.zeros((g.size, horizon, model.n_quantiles), np.float32)
     _check(lib().t0h_forecast_grouped(model.h, _p(c), _p(g), g.size, t_ctx, horizon, _p(out), out.size))
     return out
+
+
+def forecast_grouped_dev_noalloc(model, d_contexts, row_group, t_ctx, horizon, d_out):
+    """forecast_grouped_dev without any device or pinned allocation: the window's workspace is a
+    slice of the library's static per-GPU scratch (T0H_NOALLOC_SCRATCH_BYTES)."""
+    g = np.ascontiguousarray(row_group, np.int64)
+    _check(lib().t0h_forecast_grouped_dev_noalloc(model.h, C.c_void_p(d_contexts), _p(g), g.size, t_ctx, horizon,
+                                                  C.c_void_p(d_out)))
 
 
 def forecast_grouped_dev(model, d_contexts, row_group, t_ctx, horizon, d_out):

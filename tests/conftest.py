@@ -8,6 +8,11 @@ import sys
 
 import numpy as np
 import pytest
+# torch carries its own HIP/HSA runtime beside the system ROCm one libt0hip.so
+# links; both coexist in one process when torch's libraries are loaded and its
+# runtime initialized before libt0hip.so initializes HIP (the engine fixture
+# below asks for torch_cuda first), the order bench.py uses too.
+import torch  # noqa: F401
 
 ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
 for sub in ("oracle", "t0-web_amd", "tests"):
@@ -35,7 +40,7 @@ def t0hip():
 
 
 @pytest.fixture(scope="session")
-def engine(t0hip):
+def engine(t0hip, torch_cuda):
     return t0hip.Engine(0)
 
 
