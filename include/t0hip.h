@@ -53,6 +53,8 @@ enum t0h_status {
   T0H_ERR_SHAPE = -13,           /* tensor shape inconsistent with the config */
   T0H_ERR_UNSUPPORTED = -14,     /* outside this engine's documented limits */
   T0H_ERR_OOM = -15,             /* host or device allocation failed */
+  T0H_ERR_SAFETENSORS = -16,     /* weights.rs:123-129 bad safetensors file or a non-F32 tensor */
+  T0H_ERR_CONFIG = -17,          /* main.rs:285 config.json not a T0Config (serde_json error) */
 };
 
 /* ggml tensor type ids (gguf.rs:31-49) */
@@ -240,6 +242,19 @@ typedef struct {
 int t0h_synth_model_gguf(const t0h_synth_spec* spec, int quant, uint8_t* out, size_t cap, size_t* len);
 /* Re-export a GGUF's tensors with another quantization (≡ export_gguf). */
 int t0h_export_gguf(const uint8_t* bytes, size_t len, int quant, uint8_t* out, size_t cap, size_t* out_len);
+/* ≡ t0-cli export-gguf (crates/cli/src/main.rs:283-295): Weights::load_bytes of
+ * an all-F32 model.safetensors (weights.rs:115-140), the checkpoint's
+ * config.json as serde reads T0Config (config.rs:6-32; NUL-terminated UTF-8),
+ * then Weights::export_gguf (weights.rs:184-227) with quant T0H_F16, T0H_Q8_0 or
+ * T0H_Q4_0 (T0H_F32 keeps every tensor F32).  Call with out = NULL to get
+ * *out_len. */
+int t0h_export_gguf_from_safetensors(const uint8_t* st_bytes, size_t st_len, const char* config_json, int quant,
+                                     uint8_t* out, size_t cap, size_t* out_len);
+/* ≡ t0_fast::load_model(engine, weights, config, quant) (crates/t0-fast/src/lib.rs:34-36):
+ * the same export, loaded straight onto the device (T0H_F32 matrices are held
+ * as f16 rows, as for an F32 GGUF). */
+int t0h_model_load_safetensors(t0h_ctx* ctx, const uint8_t* st_bytes, size_t st_len, const char* config_json,
+                               int quant, t0h_model** out);
 
 #ifdef __cplusplus
 }

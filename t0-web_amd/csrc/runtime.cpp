@@ -1567,6 +1567,30 @@ int t0h_synth_model_gguf(const t0h_synth_spec* spec, int quant, uint8_t* out, si
   API_END
 }
 
+int t0h_export_gguf_from_safetensors(const uint8_t* st, size_t st_len, const char* config_json, int quant,
+                                     uint8_t* out, size_t cap, size_t* out_len) {
+  API_BEGIN
+  require(st && config_json && out_len, "t0h_export_gguf_from_safetensors: NULL argument");
+  std::vector<uint8_t> b = export_gguf_from_safetensors(st, st_len, config_json, quant);
+  *out_len = b.size();
+  if (out) {
+    require(cap >= b.size(), "t0h_export_gguf_from_safetensors: output buffer too small");
+    std::memcpy(out, b.data(), b.size());
+  }
+  API_END
+}
+
+int t0h_model_load_safetensors(t0h_ctx* ctx, const uint8_t* st, size_t st_len, const char* config_json, int quant,
+                               t0h_model** out) {
+  API_BEGIN
+  require(ctx && st && config_json && out, "t0h_model_load_safetensors: NULL argument");
+  *out = nullptr;
+  const std::vector<uint8_t> g = export_gguf_from_safetensors(st, st_len, config_json, quant);
+  const int rc = t0h_model_load_gguf(ctx, g.data(), g.size(), out);
+  if (rc) return rc;  // the message is already set
+  API_END
+}
+
 int t0h_export_gguf(const uint8_t* bytes, size_t len, int quant, uint8_t* out, size_t cap, size_t* out_len) {
   API_BEGIN
   require(bytes && out_len, "t0h_export_gguf: NULL argument");

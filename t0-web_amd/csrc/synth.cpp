@@ -49,12 +49,11 @@ uint64_t fnv1a(const std::string& s) {
   return h;
 }
 
-struct F32Tensor {
-  std::string name;
-  std::vector<size_t> shape;
-  std::vector<float> data;
-};
+}  // namespace
 
+// weights.rs:187-227's per-tensor policy: names sorted, the four big per-layer
+// matmuls (rank 2, is_quantizable) as `quant`, every other tensor F16 (quant =
+// F32 keeps everything F32).
 std::vector<TensorPlan> plan_export(std::vector<F32Tensor>& ts, int quant) {
   std::sort(ts.begin(), ts.end(), [](const F32Tensor& a, const F32Tensor& b) { return a.name < b.name; });
   std::vector<TensorPlan> plans;
@@ -72,8 +71,6 @@ std::vector<TensorPlan> plan_export(std::vector<F32Tensor>& ts, int quant) {
   }
   return plans;
 }
-
-}  // namespace
 
 std::vector<uint8_t> synth_model_gguf(const t0h_synth_spec& s, int quant) {
   const t0h_config& c = s.config;

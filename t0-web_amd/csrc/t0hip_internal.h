@@ -73,6 +73,18 @@ std::vector<bool> layer_types(const t0h_config& c);
 void validate_model(const GgufFile& f, const t0h_config& c);
 bool is_quantizable(const std::string& name);
 
+// An F32 tensor as Weights holds one (weights.rs:21-23).
+struct F32Tensor {
+  std::string name;
+  std::vector<size_t> shape;
+  std::vector<float> data;
+};
+// weights.rs:187-227's export policy applied to `ts` (sorted by name in place).
+std::vector<TensorPlan> plan_export(std::vector<F32Tensor>& ts, int quant);
+// model.safetensors + config.json -> GGUF bytes (main.rs:283-295 cmd_export_gguf).
+std::vector<uint8_t> export_gguf_from_safetensors(const uint8_t* st, size_t st_len, const char* config_json,
+                                                  int quant);
+
 // ---- error state ----
 void set_error(const std::string& msg);
 

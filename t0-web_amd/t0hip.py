@@ -30,6 +30,7 @@ STATUS = {
     0: "OK", -1: "INVALID_ARG", -2: "GGUF_MAGIC", -3: "GGUF_VERSION", -4: "GGUF_TENSOR_TYPE",
     -5: "GGUF_META_TYPE", -6: "GGUF_BOUNDS", -7: "MISSING_TENSOR", -8: "METADATA", -9: "HORIZON",
     -10: "FUTURE_ROWS", -11: "NO_DEVICE", -12: "HIP", -13: "SHAPE", -14: "UNSUPPORTED", -15: "OOM",
+    -16: "SAFETENSORS", -17: "CONFIG",
 }
 
 
@@ -77,7 +78,8 @@ SYMBOLS = [
     "t0h_forecast_batch_rows_chunked", "t0h_forecast_grouped", "t0h_forecast_grouped_dev",
     "t0h_forecast_grouped_dev_noalloc",
     "t0h_forecast_grouped_ar", "t0h_forecast_rollout", "t0h_dequant", "t0h_gemm_q", "t0h_gemm_f16", "t0h_row_bytes",
-    "t0h_quantize", "t0h_synth_model_gguf", "t0h_export_gguf",
+    "t0h_quantize", "t0h_synth_model_gguf", "t0h_export_gguf", "t0h_export_gguf_from_safetensors",
+    "t0h_model_load_safetensors",
 ]
 
 
@@ -126,6 +128,8 @@ def lib():
     L.t0h_quantize.argtypes = [I, P, S, P, S]
     L.t0h_synth_model_gguf.argtypes = [C.POINTER(SynthSpec), I, P, S, C.POINTER(S)]
     L.t0h_export_gguf.argtypes = [P, S, I, P, S, C.POINTER(S)]
+    L.t0h_export_gguf_from_safetensors.argtypes = [P, S, C.c_char_p, I, P, S, C.POINTER(S)]
+    L.t0h_model_load_safetensors.argtypes = [P, P, S, C.c_char_p, I, C.POINTER(P)]
     _lib = L
     return L
 
@@ -204,6 +208,18 @@ def export_gguf(gguf_bytes, quant):
     return out.tobytes()
 
 
+def export_gguf_from_safetensors(st_bytes, config_json, quant):
+    """≡ t0-cli export-gguf (crates/cli/src/main.rs:283-295): F32 model.safetensors bytes + the
+    checkpoint's config.json text -> GGUF bytes with Weights::export_gguf's policy."""
+    b = np.frombuffer(bytes(st_bytes), np.uint8)
+    cj = config_json.encode() if isinstance(config_json, str) else bytes(config_json)
+    n = C.c_size_t()
+    _check(lib().t0h_export_gguf_from_safetensors(_p(b), b.size, cj, quant, None, 0, C.byref(n)))
+    out = np.zeros(n.value, np.uint8)
+    _check(lib().t0h_export_gguf_from_safetensors(_p(b), b.size, cj, quant, _p(out), out.size, C.byref(n)))
+    return out.tobytes()
+
+
 # ---------------------------------------------------------------------------
 # Engine / GpuModel
 # ---------------------------------------------------------------------------
@@ -229,12 +245,15 @@ class GpuModel:
     """≡ t0_fast::GpuModel (crates/t0-fast/src/model.rs:170-187): resident weights + own workspace/stream.
     Calls on one model must be serialized by the caller."""
 
-    def __init__(self, engine, gguf_bytes):
+    def __init__(self, engine, gguf_bytes=None, _handle=None):
         self.engine = engine  # keep the context alive
         self._lib = lib()
-        self._bytes = np.frombuffer(bytes(gguf_bytes), np.uint8)
-        h = C.c_void_p()
-        _check(lib().t0h_model_load_gguf(engine.h, _p(self._bytes), self._bytes.size, C.byref(h)))
+        if _handle is None:
+            self._bytes = np.frombuffer(bytes(gguf_bytes), np.uint8)
+            h = C.c_void_p()
+            _check(lib().t0h_model_load_gguf(engine.h, _p(self._bytes), self._bytes.size, C.byref(h)))
+        else:
+            h = _handle
         self.h = h
         cfg = Config()
         _check(lib().t0h_model_config(self.h, C.byref(cfg)))
@@ -301,6 +320,16 @@ class GpuModel:
 def load_model_from_gguf(engine, gguf_bytes):
     """≡ t0_fast::load_model_from_gguf (lib.rs:42-44)."""
     return GpuModel(engine, gguf_bytes)
+
+
+def load_model(engine, st_bytes, config_json, quant):
+    """≡ t0_fast::load_model(engine, weights, config, quant) (lib.rs:34-36): an F32
+    model.safetensors and its config.json, big matmuls quantized as `quant`."""
+    b = np.frombuffer(bytes(st_bytes), np.uint8)
+    cj = config_json.encode() if isinstance(config_json, str) else bytes(config_json)
+    h = C.c_void_p()
+    _check(lib().t0h_model_load_safetensors(engine.h, _p(b), b.size, cj, quant, C.byref(h)))
+    return GpuModel(engine, _handle=h)
 
 
 def forward(model, variates, mask, group_ids, variate_type, trace=False):

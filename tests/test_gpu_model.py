@@ -265,6 +265,30 @@ def test_rollout(models, t0hip, oracle, engine):
     report("rollout free-running drift", got, want, sc)
 
 
+@pytest.mark.parametrize("q", [8, 2])
+def test_load_model_from_safetensors(t0hip, oracle, engine, rng, q):
+    """t0_fast::load_model(engine, weights, config, quant) (lib.rs:34-36): an F32 model.safetensors
+    (written by the safetensors package) and its config.json straight onto the device; forecasts
+    equal those of the GGUF the same export writes (loaded through t0h_model_load_gguf), and match
+    the oracle on that GGUF."""
+    import json
+    import safetensors.numpy
+    from test_oracle import _tensor_names
+    g32 = t0hip.synth_model_gguf(t0hip.make_config(**SMALL), quant=0, seed=23)
+    om32 = oracle.Model(g32)
+    st = safetensors.numpy.save({n: np.ascontiguousarray(om32.tensor(n)) for n in _tensor_names(g32)})
+    cj = json.dumps({k: SMALL[k] for k in ("embed_dim", "num_layers", "num_heads", "mlp_hidden_dim", "patch_size",
+                                           "group_every_n")} |
+                    {"dropout": 0.0, "quantile_levels": [float(np.float32(x)) for x in SMALL["quantile_levels"]]})
+    gm = t0hip.load_model(engine, st, cj, q)
+    gguf = t0hip.export_gguf_from_safetensors(st, cj, q)
+    ref = t0hip.load_model_from_gguf(engine, gguf)
+    ctx = nan_gaps(rng, sine_mix(rng, 3, 700))
+    got = t0hip.forecast(engine, gm, ctx, 3, 700, 64)
+    assert np.array_equal(got, t0hip.forecast(engine, ref, ctx, 3, 700, 64))
+    assert_close(got, oracle.Model(gguf).forecast(ctx, 3, 700, 64), scale=row_scale(ctx))
+
+
 def test_two_models_interleaved_bit_identical(t0hip, engine, rng):
     """t0-fast tests/pool_isolation.rs:43-84: two models on one engine, calls A,B,A,B are
     bit-identical to isolated runs (each model owns its workspace)."""
