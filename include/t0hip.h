@@ -214,8 +214,9 @@ int t0h_gemm_q(int wtype, const void* d_w, const float* d_x, const float* d_bias
  * tile: 0 = as the forward picks, 1 = 128x128, 3 = 256x256, 4 = 256x256 with
  * DMA-fed activations (K % 128 == 0, quantized weights; falls back to 1),
  * 5 = 256x256 with the weights dequantized straight into MFMA operands,
- * 6 = the same with 256x128 tiles and two workgroups per CU (5 and 6:
- * K % 64 == 0, quantized weights; fall back to 1). */
+ * 6 = the same with 256x128 tiles and two workgroups per CU, 7 / 8 = the
+ * same with 192x128 / 128x128 tiles (5-8: K % 64 == 0, quantized weights;
+ * fall back to 1). */
 int t0h_gemm_f16(int wtype, const void* d_w, const void* d_x, const float* d_bias, void* d_y, size_t m, size_t n,
                  size_t k, int epilogue, int tile, void* stream);
 

@@ -947,16 +947,21 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1))) voi
 //    overlapping it, and bursts of loads right after a barrier stall issue.
 // ---------------------------------------------------------------------------
 constexpr int BF_BM = 256;
-constexpr int BF_ABUF = BF_BM * LDK;  // halves per activation buffer
 // NWV waves of 32 weight columns each; 8 waves: three activation buffers
 // (110,592 bytes, one workgroup per CU), 4 waves: two (73,728 bytes, two
 // workgroups per CU, so one's epilogue overlaps the other's main loop).
-template <int NWV>
+template <int NWV, int BM = BF_BM>
 struct BfCfg {
-  static constexpr int BN = 32 * NWV, NBUF = NWV == 8 ? 3 : 2, LDS = NBUF * BF_ABUF * 2;
+  static constexpr int BN = 32 * NWV, NBUF = NWV == 8 ? 3 : 2, ABUF = BM * LDK, LDS = NBUF * ABUF * 2;
 };
 
 typedef uint32_t u32x8 __attribute__((ext_vector_type(8)));
+// The dequantization sub-step (0..3) that follows MFMA i of a TI-MFMA slice, or -1.
+__host__ __device__ constexpr int dq_sub_at(int i, int TI) {
+  for (int q = 0; q < 4; ++q)
+    if ((q * TI) / 4 == i) return q;
+  return -1;
+}
 // An activation chunk as f16 for the LDS tile: f16 chunks as they are, f32
 // chunks (8 values) rounded to f16.
 __device__ __forceinline__ u32x4 a_f16(u32x4 r) { return r; }
@@ -967,20 +972,20 @@ __device__ __forceinline__ u32x4 a_f16(u32x8 r) {
   return __builtin_bit_cast(u32x4, h);
 }
 
-template <int WT, int EPI, int NWV, bool A32>
+template <int WT, int EPI, int NWV, bool A32, int BM>
 __global__ __launch_bounds__(64 * NWV) __attribute__((amdgpu_waves_per_eu(2, 2))) void k_gemm_bf(const GemmDesc d) {
-  using C = BfCfg<NWV>;
-  constexpr int BN = C::BN, NBUF = C::NBUF;
-  constexpr int TI = BF_BM / 32, TJ = 1;      // 32x32 tiles per wave
-  constexpr int ACH = 2048 / (64 * NWV);      // 16-byte activation chunks per thread and step
-  constexpr int AQS = BF_BM / ACH;            // row stride between a thread's chunks
+  using C = BfCfg<NWV, BM>;
+  constexpr int BN = C::BN, NBUF = C::NBUF, BF_ABUF = C::ABUF;
+  constexpr int TI = BM / 32, TJ = 1;         // 32x32 tiles per wave
+  constexpr int ACH = BM * 8 / (64 * NWV);    // 16-byte activation chunks per thread and step
+  constexpr int AQS = BM / ACH;               // row stride between a thread's chunks
   constexpr int NMI = 4 * TI;                 // MFMAs per step
   constexpr int RING = 8, RD = 6;             // A fragment ring; RING divides NMI
   constexpr bool SWI = EPI == EPI_SWIGLU_F16;
   constexpr int HB = SWI ? BN / 2 : BN;          // output columns per tile
   constexpr int NWD = WT == T0H_Q8_0 ? 9 : 5;    // raw dwords a lane needs per step
   constexpr int SWD = WT == T0H_Q8_0 ? 17 : 9;   // dwords of one row's two blocks (one step)
-  static_assert(NMI % RING == 0 && RD < RING && ACH <= TI, "step work placement");
+  static_assert(NMI % RING == 0 && RD < RING && ACH <= TI && TI >= 4, "step work placement");
   static_assert(NWV * 32 * ((SWI ? 16 : 32) + 4) * 4 <= C::LDS, "epilogue stage fits the LDS");
   extern __shared__ __align__(16) _Float16 smem[];
 
@@ -993,7 +998,7 @@ __global__ __launch_bounds__(64 * NWV) __attribute__((amdgpu_waves_per_eu(2, 2))
   // tiles share activation rows in that XCD's L2.
   const int total = gridDim.x, bid = blockIdx.x, per = total / 8;
   const int t = bid < per * 8 ? (bid % 8) * per + bid / 8 : bid;
-  const int tn = t % tiles_n, m0 = (t / tiles_n) * BF_BM;
+  const int tn = t % tiles_n, m0 = (t / tiles_n) * BM;
 
   // Activation chunk t%8 of rows t/8 + AQS q (rows past M read row M-1,
   // never stored) as byte offsets from the tile's first row; the lane's weight
@@ -1105,7 +1110,7 @@ __global__ __launch_bounds__(64 * NWV) __attribute__((amdgpu_waves_per_eu(2, 2))
   // One step: slice c, MFMA i (m = c*TI + i): the ring read of fragment
   // m + RD (with three buffers, in step kt+1 once past the step: its buffer
   // is complete; with two, the next step reads its first RD fragments after
-  // the barrier), B sub-steps after every other MFMA, the activation chunk
+  // the barrier), B sub-steps spread over the slice (every other MFMA at 256 rows), the activation chunk
   // loads of step kt+NBUF-1 and the W(kt+1) load early in the first slices
   // (W first when the ACH = 8 chunk loads would push it into the second
   // slice: its data is needed in the last), the activation stores in the
@@ -1138,11 +1143,24 @@ __global__ __launch_bounds__(64 * NWV) __attribute__((amdgpu_waves_per_eu(2, 2))
           ring[mr % RING] = read_a(b1, 0, mr - NMI);
         if (m == WPOS) load_b(nxt, kb);
         if (!EARLY && m >= A0 && m < A0 + ACH) load_a(ar[m - A0], ka, m - A0);
-        if ((i & 1) == 0) {
-          if (c < 3)
-            dq(cur, c + 1, i >> 1, bf[n]);
-          else
-            dq(nxt, 0, i >> 1, bf[n]);
+        // the four dequantization sub-steps of the next slice's B fragment, spread over the
+        // slice's TI MFMAs: after every other MFMA at TI = 8, sub-step q after MFMA (q * TI) / 4
+        // otherwise
+        if constexpr (TI == 8) {
+          if ((i & 1) == 0) {
+            if (c < 3)
+              dq(cur, c + 1, i >> 1, bf[n]);
+            else
+              dq(nxt, 0, i >> 1, bf[n]);
+          }
+        } else {
+          const int q = dq_sub_at(i, TI);
+          if (q >= 0) {
+            if (c < 3)
+              dq(cur, c + 1, q, bf[n]);
+            else
+              dq(nxt, 0, q, bf[n]);
+          }
         }
         if (c == 3 && i < ACH) {
           *a_dst(NBUF == 3 ? b2 : b1, i) = a_f16(ar[i]);
@@ -1713,14 +1731,14 @@ void run_gemm_dma(const GemmDesc& d, hipStream_t s) {
   check_hip(hipGetLastError(), "k_gemm_dma launch");
 }
 
-template <int WT, int EPI, int NWV, bool A32 = false>
+template <int WT, int EPI, int NWV, bool A32 = false, int BM = BF_BM>
 void run_gemm_bf(const GemmDesc& d, hipStream_t s) {
-  using C = BfCfg<NWV>;
+  using C = BfCfg<NWV, BM>;
   const int hb = EPI == EPI_SWIGLU_F16 ? C::BN / 2 : C::BN;
-  const int n_tiles = ((d.N + hb - 1) / hb) * ((d.M + BF_BM - 1) / BF_BM);
+  const int n_tiles = ((d.N + hb - 1) / hb) * ((d.M + BM - 1) / BM);
   static std::atomic<uint64_t> lds_set{0};  // per instantiation
-  allow_dynamic_lds(reinterpret_cast<const void*>(&k_gemm_bf<WT, EPI, NWV, A32>), lds_set);
-  hipLaunchKernelGGL((k_gemm_bf<WT, EPI, NWV, A32>), dim3(n_tiles), dim3(64 * NWV), C::LDS, s, d);
+  allow_dynamic_lds(reinterpret_cast<const void*>(&k_gemm_bf<WT, EPI, NWV, A32, BM>), lds_set);
+  hipLaunchKernelGGL((k_gemm_bf<WT, EPI, NWV, A32, BM>), dim3(n_tiles), dim3(64 * NWV), C::LDS, s, d);
   check_hip(hipGetLastError(), "k_gemm_bf launch");
 }
 
@@ -1732,6 +1750,11 @@ void run_gemm_tiled(const GemmDesc& d, int tile, hipStream_t s) {
   // w2 224 / 232 / 238 (standalone).  Inside the forward QKV measured 213.5 us
   // on the 256x128 kernel against 217.5 on the 256x256 one, so it takes the
   // 256x128 kernel too.  The DMA and plain 256x256 tiles lose at every shape.
+  // 192- and 128-row tiles (7, 8), which would fill the last round of the
+  // N = 768 launches better (1,188 tiles are 2.32 rounds of 512 slots), measured
+  // slower inside the config-4 forward at every layer GEMM (Q4_0 step 12.80 ->
+  // 13.24 / 13.73 ms; Q8_0 13.47 -> 14.12 / 14.81): each weight fragment then
+  // feeds 6 or 4 MFMAs instead of 8.
   // Below ~1024 rows a 256-row tile is mostly padding.
   if (tile == 0) {
     tile = 1;
@@ -1746,6 +1769,8 @@ void run_gemm_tiled(const GemmDesc& d, int tile, hipStream_t s) {
     if (tile == 4 && dma_ok(d)) return run_gemm_dma<WT, EPI>(d, s);
     if (tile == 5) return run_gemm_bf<WT, EPI, 8>(d, s);
     if (tile == 6) return run_gemm_bf<WT, EPI, 4>(d, s);
+    if (tile == 7) return run_gemm_bf<WT, EPI, 4, false, 192>(d, s);
+    if (tile == 8) return run_gemm_bf<WT, EPI, 4, false, 128>(d, s);
   }
   if constexpr (!A32 && K64) {
     if (tile == 3 || tile == 4) return run_gemm<WT, A32, EPI, K64, 4, 4>(d, s);
@@ -1882,9 +1907,9 @@ void dispatch_w(const GemmDesc& d, int force, hipStream_t s) {
   if constexpr (WT != T0H_F16) {
     // medium M (force 0) or force 9
     const bool mid = force == 0 && d.M > 16 && d.M < MID_M_MAX && (long long)d.M * d.N <= MID_MN_MAX;
-    if ((force == 9 || mid) && mid_ok(d)) return dispatch_mid<WT, A32, EPI>(d, s);
+    if ((force == FORCE_MID || mid) && mid_ok(d)) return dispatch_mid<WT, A32, EPI>(d, s);
   }
-  const bool mfma = force == 1 || (force >= 3 && force != 9) || (force == 0 && d.M > 16);
+  const bool mfma = force == 1 || (force >= 3 && force != FORCE_MID) || (force == 0 && d.M > 16);
   if (mfma) {
     const int tile = force >= 3 ? force - 2 : 0;
     if (d.K % 64 == 0)

@@ -53,8 +53,10 @@ void launch_gemm(const GemmDesc& d, hipStream_t s);
 // medium-M kernel up to 512 x 2304 outputs; else MFMA tiles); 1: MFMA tile kernel (tile
 // by shape); 2: small-M kernels; 3 / 4 / 5: MFMA kernel with 128x128 / 256x128 / 256x256
 // tiles; 6: 256x256 DMA-fed kernel; 7 / 8: 256x256 / 256x128 kernels with
-// register-dequantized weight fragments (6-8: K % 64 == 0, f16 activations, quantized
-// weights); 9: medium-M kernel (K % 64 == 0, quantized weights).
+// register-dequantized weight fragments, 9 / 10: the 256x128 one with 192 / 128 rows (6-10:
+// K % 64 == 0, f16 activations, quantized weights); FORCE_MID: medium-M kernel (K % 64 == 0,
+// quantized weights).
+constexpr int FORCE_MID = 32;
 void launch_gemm_forced(const GemmDesc& d, int force, hipStream_t s);
 void launch_dequant(int type, const void* w, size_t n, float* out, hipStream_t s);
 

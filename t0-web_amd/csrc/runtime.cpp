@@ -1525,7 +1525,7 @@ int t0h_gemm_f16(int wtype, const void* d_w, const void* d_x, const float* d_bia
   API_BEGIN
   require(m < (1u << 31) && n < (1u << 31) && k < (1u << 31), "t0h_gemm_f16: dimension too large");
   require(epilogue >= EPI_STORE_F32 && epilogue <= EPI_SWIGLU_F16, "t0h_gemm_f16: unknown epilogue");
-  require(tile >= 0 && tile <= 6 && tile != 2, "t0h_gemm_f16: tile must be 0, 1 or 3..6");
+  require(tile >= 0 && tile <= 8 && tile != 2, "t0h_gemm_f16: tile must be 0, 1 or 3..8");
   GemmDesc d;
   d.wtype = wtype;
   d.w = d_w;

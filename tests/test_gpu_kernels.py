@@ -194,7 +194,7 @@ def check_forward_gemm(torch, t0hip, oracle, rng, qtype, tile, epi, m, k, n, sam
 
 
 @pytest.mark.parametrize("qtype", [8, 2])
-@pytest.mark.parametrize("tile", [1, 3, 4, 5, 6])
+@pytest.mark.parametrize("tile", [1, 3, 4, 5, 6, 7, 8])
 @pytest.mark.parametrize("epi", [0, 1, 2, 3])
 def test_forward_gemm_paths(torch_cuda, t0hip, oracle, rng, qtype, tile, epi):
     """linear() (model.rs:406-504) as the forward runs it: f16 x, f32 accumulation,
@@ -205,11 +205,11 @@ def test_forward_gemm_paths(torch_cuda, t0hip, oracle, rng, qtype, tile, epi):
 
 
 @pytest.mark.parametrize("qtype", [8, 2])
-@pytest.mark.parametrize("tile", [5, 6])
+@pytest.mark.parametrize("tile", [5, 6, 7, 8])
 @pytest.mark.parametrize("epi", [0, 1, 2, 3])
 @pytest.mark.parametrize("m,k,n", [(300, 192, 328), (257, 64, 330), (40, 128, 72)])
 def test_register_b_gemm_edges(torch_cuda, t0hip, oracle, rng, qtype, tile, epi, m, k, n):
-    """The register-operand kernels (tiles 5 and 6) on partial tiles: M and N
+    """The register-operand kernels (tiles 5-8: 256, 192 and 128 rows) on partial tiles: M and N
     ragged (weight rows past N clamp to row 0), an odd number of 64-wide K steps
     (the step after the paired loop), one step, and N % 4 != 0 (scalar stores;
     SwiGLU needs N % 8 == 0 and takes n rounded down to 8)."""
