@@ -71,7 +71,7 @@ __device__ __forceinline__ void load_f8(const float* t, float* a) {
   a[0] = u.x, a[1] = u.y, a[2] = u.z, a[3] = u.w, a[4] = w.x, a[5] = w.y, a[6] = w.z, a[7] = w.w;
 }
 
-// One workgroup per (variate row, head), TA_WAVES waves.
+// One workgroup (qsplit of them for few rows) per (variate row, head), TA_WAVES waves.
 // Key phase: 8 lanes per 64-wide k row (16 B each), QK-RMSNorm reduced over
 // the 8-lane group, norm scale + interleaved xPos RoPE from the folded tables,
 // keys stored row-major; v rows in key pairs, transposed into LDS as
@@ -92,7 +92,11 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(MAXKT <= 8 
   int* Kg = reinterpret_cast<int*>(Os + TA_WAVES * 16 * LDH);
 
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6, part = lane >> 4;
-  const int r = blockIdx.x / d.heads, h = blockIdx.x % d.heads;
+  // qsplit workgroups share a (row, head): each loads every key and takes every
+  // qsplit-th wave slot of the query tiles
+  const int S = d.qsplit, sp = blockIdx.x % S, rh = blockIdx.x / S;
+  const int r = rh / d.heads, h = rh % d.heads;
+  const int NW = TA_WAVES * S, wv = wave * S + sp;
   const int E = d.E, ld = 3 * E;
   const size_t row0 = (size_t)r * p;
   const _Float16* qb = d.qkv + row0 * ld + h * HD;  // q; k at +E, v at +2E
@@ -100,7 +104,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(MAXKT <= 8 
 
   // This wave's j-th tile in cost order (the snake over waves); -1 when past the last.
   auto tile_at = [&](int k) {
-    const int j = (k >> 1) * 2 * TA_WAVES + ((k & 1) ? 2 * TA_WAVES - 1 - wave : wave);
+    const int j = (k >> 1) * 2 * NW + ((k & 1) ? 2 * NW - 1 - wv : wv);
     return j < nqt ? nqt - 1 - j : -1;
   };
   auto load_q = [&](int qt, uint4& a, uint4& b) {
@@ -491,7 +495,7 @@ template <int MAXKT>
 void run_time_attn(const AttnDesc& d, size_t lds, hipStream_t s) {
   static std::atomic<uint64_t> lds_set{0};  // per instantiation
   allow_dynamic_lds(reinterpret_cast<const void*>(&k_time_attn<MAXKT>), lds_set);
-  hipLaunchKernelGGL(k_time_attn<MAXKT>, dim3(d.v * d.heads), dim3(TA_WAVES * 64), lds, s, d);
+  hipLaunchKernelGGL(k_time_attn<MAXKT>, dim3(d.v * d.heads * d.qsplit), dim3(TA_WAVES * 64), lds, s, d);
 }
 
 }  // namespace
@@ -506,14 +510,19 @@ void launch_time_attention(const AttnDesc& d, hipStream_t s) {
   static_assert(T0H_MAX_PATCHES <= 16 * 16, "the largest instance covers 16 key tiles of 16");
   const size_t lds = time_attn_lds(d.p);
   const int kt = round_up(d.p, 32) / 16;
+  // Few (row, head) pairs (one or two series): split each one's query tiles over
+  // up to one workgroup per tile so that about a round of the CUs is busy.
+  AttnDesc dd = d;
+  const int nqt = round_up(d.p, 16) / 16, pairs = d.v * d.heads;
+  dd.qsplit = std::max(1, std::min(nqt, 256 / std::max(1, pairs)));
   if (kt <= 4)
-    run_time_attn<4>(d, lds, s);
+    run_time_attn<4>(dd, lds, s);
   else if (kt <= 8)
-    run_time_attn<8>(d, lds, s);
+    run_time_attn<8>(dd, lds, s);
   else if (kt <= 12)
-    run_time_attn<12>(d, lds, s);
+    run_time_attn<12>(dd, lds, s);
   else
-    run_time_attn<16>(d, lds, s);
+    run_time_attn<16>(dd, lds, s);
   check_hip(hipGetLastError(), "k_time_attn launch");
 }
 

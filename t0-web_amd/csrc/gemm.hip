@@ -1861,7 +1861,7 @@ int device_cus() {
 }
 
 // Shapes the medium-M kernel takes: K % 64 == 0 and K <= 4096 (f16 activations)
-// or 2048 (f32); 32-row tiles for f32 activations or M <= 32, else 64.  From
+// or 2048 (f32); 32-row tiles for f32 activations or M < 256, else 64.  From
 // 256 rows (and not SwiGLU) a workgroup may cover four or two 32-column groups
 // (two past K = 1024), so the activation block is read by a quarter or half as
 // many workgroups, when that still fills about one round of the CUs.
@@ -1891,7 +1891,10 @@ void dispatch_mid(const GemmDesc& d, hipStream_t s) {
       }
     }
   }
-  if (A32 || d.M <= 32 || KT > 32) {
+  // 32-row tiles below 256 rows: more workgroups, each with a shorter operand
+  // set (measured at M = 66 / 198, Q8_0: w2 14.0 -> 9.9 / 14.2 -> 10.2 us, QKV
+  // 6.9 -> 5.9, wO 6.8 -> 5.9, SwiGLU 7.2 -> 6.8 / 11.6 -> 10.7 us)
+  if (A32 || d.M < 256 || KT > 32) {
     if (KT <= 16) return run_gemm_mid<WT, A32, EPI, 1, 2>(d, s);
     if (KT <= 32) return run_gemm_mid<WT, A32, EPI, 1, 4>(d, s);
     if constexpr (!A32) return run_gemm_mid<WT, A32, EPI, 1, 8>(d, s);

@@ -84,6 +84,7 @@ struct AttnDesc {
   const int* seg_begin = nullptr;    // [v]
   const int* seg_len = nullptr;      // [v]
   int seg_max = 0;                   // longest segment (selects the kernel)
+  int qsplit = 1;                    // time attention: workgroups per (row, head), set by the launcher
 };
 void launch_time_attention(const AttnDesc& d, hipStream_t s);
 void launch_group_attention(const AttnDesc& d, hipStream_t s);
