@@ -1779,6 +1779,169 @@ void run_gemm_tiled(const GemmDesc& d, int tile, hipStream_t s) {
   run_gemm<WT, A32, EPI, K64, 2, 2>(d, s);
 }
 
+// ---------------------------------------------------------------------------
+// Small-M kernel for 2 <= M <= 16 rows (any weight type, K % 32 == 0): exact
+// f32 products on v_mfma_f32_16x16x4f32.  A workgroup owns 16 weight rows
+// (SwiGLU: 8 gate rows and their 8 up rows) and splits K over MF_WAVES waves,
+// block kb going to wave kb % MF_WAVES.  In a 32-value block, lane (j, c) =
+// (lane % 16, lane / 16) dequantizes values 8c .. 8c+7 of weight row j exactly
+// (f32(d) * q: an 11-bit scale times an integer of at most 8 bits; f16 weights
+// convert exactly) and holds activations 8c .. 8c+7 of row j; MFMA s of the
+// block takes value 8c + s from every lane, so each product of the block is
+// summed once.  The waves' 16x16 partial tiles are summed in LDS in wave order
+// and written by one thread per output (bias, ReLU, residual add or SwiGLU).
+// The weights are read with 2-byte loads (Q8_0 / Q4_0 blocks are 2-byte
+// aligned), never past a block.
+// ---------------------------------------------------------------------------
+constexpr int MF_WAVES = 8, MF_CH = 4;  // waves per workgroup, blocks per load batch
+
+template <int WT, bool A32, int EPI>
+__global__ __launch_bounds__(64 * MF_WAVES) void k_gemv_mf(const GemmDesc d) {
+  __shared__ float red[MF_WAVES][16][17];
+  constexpr bool SWI = EPI == EPI_SWIGLU_F16;
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6, j = lane & 15, c = lane >> 4;
+  const int M = d.M, N = d.N, K = d.K, KB = K / 32;
+  const int c0 = blockIdx.x * (SWI ? 8 : 16);  // first output column (SwiGLU: hidden unit)
+  int wrow;
+  if (SWI) {
+    const int u = min(c0 + (j & 7), N - 1);
+    wrow = j < 8 ? u : N + u;
+  } else {
+    wrow = min(c0 + j, N - 1);  // rows past N are computed, never stored
+  }
+  const size_t rowb = WT == T0H_F16 ? (size_t)K * 2 : (size_t)KB * block_bytes(WT);
+  const uint8_t* wr = static_cast<const uint8_t*>(d.w) + (size_t)wrow * rowb;
+  const bool arow = j < M;
+  const size_t aoff = (size_t)(arow ? j : 0) * d.lda + 8 * c;
+
+  // one block's operands for this lane: 8 weights (raw) and 8 activations
+  struct Op {
+    uint32_t w[4];  // Q8_0 / Q4_0: 4 x 2 bytes (+ the scale in sc); f16: 8 halves
+    uint32_t sc;
+    uint32_t a[A32 ? 8 : 4];
+  };
+  auto load = [&](int kb, Op& o) {
+    if constexpr (WT == T0H_F16) {
+      const uint4 v = *reinterpret_cast<const uint4*>(wr + (size_t)(kb * 32 + 8 * c) * 2);
+      o.w[0] = v.x, o.w[1] = v.y, o.w[2] = v.z, o.w[3] = v.w;
+      o.sc = 0;
+    } else {
+      const uint8_t* b = wr + (size_t)kb * block_bytes(WT);
+      const uint16_t* q = reinterpret_cast<const uint16_t*>(b + 2 + (WT == T0H_Q8_0 ? 8 * c : 8 * (c & 1)));
+#pragma unroll
+      for (int e = 0; e < 4; ++e) o.w[e] = q[e];
+      o.sc = *reinterpret_cast<const uint16_t*>(b);
+    }
+    if (arow) {
+      if constexpr (A32) {
+        const float4* x = reinterpret_cast<const float4*>(static_cast<const float*>(d.a) + aoff + (size_t)kb * 32);
+        const float4 x0 = x[0], x1 = x[1];
+        o.a[0] = __float_as_uint(x0.x), o.a[1] = __float_as_uint(x0.y), o.a[2] = __float_as_uint(x0.z);
+        o.a[3] = __float_as_uint(x0.w), o.a[4] = __float_as_uint(x1.x), o.a[5] = __float_as_uint(x1.y);
+        o.a[6] = __float_as_uint(x1.z), o.a[7] = __float_as_uint(x1.w);
+      } else {
+        const uint4 v = *reinterpret_cast<const uint4*>(static_cast<const _Float16*>(d.a) + aoff + (size_t)kb * 32);
+        o.a[0] = v.x, o.a[1] = v.y, o.a[2] = v.z, o.a[3] = v.w;
+      }
+    } else {
+#pragma unroll
+      for (int e = 0; e < (A32 ? 8 : 4); ++e) o.a[e] = 0;
+    }
+  };
+  auto weight = [&](const Op& o, int s) -> float {
+    if constexpr (WT == T0H_F16) {
+      return (float)__builtin_bit_cast(half2v, o.w[s >> 1])[s & 1];
+    } else {
+      const float dd = (float)__builtin_bit_cast(_Float16, (uint16_t)o.sc);
+      const uint32_t byte = (o.w[s >> 1] >> (8 * (s & 1))) & 0xffu;
+      if constexpr (WT == T0H_Q8_0) return dd * (float)(int8_t)byte;
+      const uint32_t nib = c >= 2 ? byte >> 4 : byte & 15u;
+      return dd * (float)((int)nib - 8);
+    }
+  };
+  auto act = [&](const Op& o, int s) -> float {
+    if constexpr (A32) return __uint_as_float(o.a[s]);
+    return (float)__builtin_bit_cast(half2v, o.a[s >> 1])[s & 1];
+  };
+
+  floatx4 acc = {0.0f, 0.0f, 0.0f, 0.0f};
+  // batches of MF_CH blocks, the next batch's loads issued before this one's MFMAs
+  Op ops[2][MF_CH];
+  auto load_batch = [&](int kb0, Op(&o)[MF_CH]) {
+#pragma unroll
+    for (int q = 0; q < MF_CH; ++q)
+      if (kb0 + q * MF_WAVES < KB) load(kb0 + q * MF_WAVES, o[q]);
+  };
+  auto run_batch = [&](int kb0, const Op(&o)[MF_CH]) {
+#pragma unroll
+    for (int q = 0; q < MF_CH; ++q)
+      if (kb0 + q * MF_WAVES < KB) {
+#pragma unroll
+        for (int s = 0; s < 8; ++s)
+          acc = __builtin_amdgcn_mfma_f32_16x16x4f32(act(o[q], s), weight(o[q], s), acc, 0, 0, 0);
+      }
+  };
+  constexpr int STEP = MF_WAVES * MF_CH;
+  load_batch(wave, ops[0]);
+  int kb0 = wave;
+  for (; kb0 + STEP < KB; kb0 += 2 * STEP) {  // pairs of batches: the buffers alternate
+    load_batch(kb0 + STEP, ops[1]);
+    run_batch(kb0, ops[0]);
+    if (kb0 + 2 * STEP < KB) load_batch(kb0 + 2 * STEP, ops[0]);
+    run_batch(kb0 + STEP, ops[1]);
+  }
+  if (kb0 < KB) run_batch(kb0, ops[0]);
+  // D layout: lane l, register r -> row 4 (l / 16) + r, column l % 16
+#pragma unroll
+  for (int r = 0; r < 4; ++r) red[wave][4 * c + r][j] = acc[r];
+  __syncthreads();
+  if (tid >= 256) return;
+  const int m = tid >> 4, jj = tid & 15;
+  if (m >= M) return;
+  float v = 0.0f;
+#pragma unroll
+  for (int w = 0; w < MF_WAVES; ++w) v += red[w][m][jj];
+  if constexpr (SWI) {
+    const int u = c0 + jj;
+    if (jj >= 8 || u >= N) return;
+    float up = 0.0f;
+#pragma unroll
+    for (int w = 0; w < MF_WAVES; ++w) up += red[w][m][jj + 8];
+    const float g = v + (d.bias ? d.bias[u] : 0.0f), uu = up + (d.bias ? d.bias[N + u] : 0.0f);
+    static_cast<_Float16*>(d.y)[(size_t)m * d.ldy + u] = (_Float16)(silu(g) * uu);
+  } else {
+    const int n = c0 + jj;
+    if (n >= N) return;
+    v += d.bias ? d.bias[n] : 0.0f;
+    if (d.relu) v = fmaxf(v, 0.0f);
+    const size_t o = (size_t)m * d.ldy + n;
+    if constexpr (EPI == EPI_RESID_F32) {
+      float* y = static_cast<float*>(d.y) + o;
+      *y = *y + v;
+    } else if constexpr (EPI == EPI_STORE_F32) {
+      static_cast<float*>(d.y)[o] = v;
+    } else {
+      static_cast<_Float16*>(d.y)[o] = (_Float16)v;
+    }
+  }
+}
+
+template <int WT, bool A32, int EPI>
+void run_gemv_mf(const GemmDesc& d, hipStream_t s) {
+  const int per = EPI == EPI_SWIGLU_F16 ? 8 : 16;
+  hipLaunchKernelGGL((k_gemv_mf<WT, A32, EPI>), dim3((d.N + per - 1) / per), dim3(64 * MF_WAVES), 0, s, d);
+  check_hip(hipGetLastError(), "k_gemv_mf launch");
+}
+
+// The f32-MFMA small-M kernel's operand loads: 16-byte activation chunks and,
+// for f16 weights, 16-byte weight chunks; no table row add.
+bool gemv_mf_ok(const GemmDesc& d) {
+  const bool a16 = (reinterpret_cast<uintptr_t>(d.a) & 15) == 0 && d.lda % (d.a_f32 ? 4 : 8) == 0;
+  const bool w16 = d.wtype != T0H_F16 || (reinterpret_cast<uintptr_t>(d.w) & 15) == 0;
+  const bool w2 = (reinterpret_cast<uintptr_t>(d.w) & 1) == 0;
+  return d.M >= 2 && d.M <= 16 && d.K % 32 == 0 && a16 && w16 && w2 && !d.row_add;
+}
+
 template <int WT, bool A32, int EPI, int MT>
 void run_gemv(const GemmDesc& d, hipStream_t s) {
   const size_t rb = WT == T0H_F16 ? (size_t)d.K * 2 : (size_t)(d.K / 32) * block_bytes(WT);
@@ -1814,6 +1977,9 @@ void dispatch_gemv_s(const GemmDesc& d, hipStream_t s) {
 
 template <int WT, bool A32, int EPI>
 void dispatch_gemv(const GemmDesc& d, hipStream_t s) {
+  // 2..16 rows: exact f32 on the f32 MFMA (the LDS-staged f32 kernels below redo
+  // every activation row per weight row: M = 16 took 10 us at K = 768, N = 2304)
+  if (gemv_mf_ok(d)) return run_gemv_mf<WT, A32, EPI>(d, s);
   if constexpr (WT != T0H_F16) {
     if (d.M <= 16 && d.K % 64 == 0 && d.K <= 4 * GS_TILE) {
       if (d.M == 1) return dispatch_gemv_s<WT, A32, EPI, 1>(d, s);

@@ -221,7 +221,7 @@ def test_register_b_gemm_edges(torch_cuda, t0hip, oracle, rng, qtype, tile, epi,
 @pytest.mark.parametrize("qtype", [8, 2])
 @pytest.mark.parametrize("m,k,n", [(1, 2560, 200), (4, 4096, 72), (16, 768, 40), (7, 2048, 17), (16, 1088, 24)])
 def test_small_m_kernel(torch_cuda, t0hip, oracle, rng, qtype, m, k, n):
-    """The small-M kernel (M <= 16, K % 64 == 0, K <= 4096) through t0h_gemm_q:
+    """The small-M kernels (M = 1: 16 lanes per weight row; 2..16: the f32 MFMA) through t0h_gemm_q:
     exact f32 dequantization and accumulation, so the 1e-5 gate of the
     reference's f32 kernels holds; a partial last K tile (K = 2560, 1088), N not
     a multiple of the 16 weight rows of a workgroup."""
@@ -237,12 +237,30 @@ def test_small_m_kernel(torch_cuda, t0hip, oracle, rng, qtype, m, k, n):
     assert rel_err(got, np.maximum(want, 0.0)) < 1e-5, (m, k, n)
 
 
-@pytest.mark.parametrize("qtype", [8, 2])
+@pytest.mark.parametrize("qtype", [8, 2, 1])
+@pytest.mark.parametrize("m,k,n", [(2, 96, 40), (3, 160, 33), (5, 4096, 300), (16, 32, 17), (12, 1056, 24),
+                                   (16, 4096, 2048)])
+def test_small_m_f32_mfma_kernel(torch_cuda, t0hip, oracle, rng, qtype, m, k, n):
+    """The 2..16-row kernel on the f32 MFMA through t0h_gemm_q: every weight type, K % 64 == 32, one
+    block (K = 32: seven of the eight waves get none), K split over the waves with a partial last
+    batch, ragged N; exact f32 products, so the reference's 1e-5 gate holds, with and without ReLU."""
+    W = (0.02 * rng.standard_normal((n, k))).astype(np.float32)
+    x = rng.standard_normal((m, k)).astype(np.float32)
+    b = (0.02 * rng.standard_normal(n)).astype(np.float32)
+    blocks = oracle.quantize(qtype, W)
+    deq = oracle.dequantize(qtype, blocks, n * k).reshape(n, k).astype(np.float64)
+    want = x.astype(np.float64) @ deq.T + b
+    assert rel_err(run_gemm(torch_cuda, t0hip, qtype, blocks, x, b, n), want) < 1e-5, (m, k, n)
+    assert rel_err(run_gemm(torch_cuda, t0hip, qtype, blocks, x, b, n, act=1), np.maximum(want, 0.0)) < 1e-5
+
+
+@pytest.mark.parametrize("qtype", [8, 2, 1])
 @pytest.mark.parametrize("epi", [0, 1, 2, 3])
-@pytest.mark.parametrize("m,k,n", [(1, 768, 136), (9, 2048, 72), (16, 768, 40)])
+@pytest.mark.parametrize("m,k,n", [(1, 768, 136), (9, 2048, 72), (16, 768, 40), (2, 96, 24)])
 def test_small_m_forward_epilogues(torch_cuda, t0hip, oracle, rng, qtype, epi, m, k, n):
-    """The forward's GEMMs at M <= 16 (a single series): f16 activations, epilogues
-    bias / f16 store / residual add / SwiGLU on the small-M kernel."""
+    """The forward's GEMMs at M <= 16 (a single series, the decoder's forecast rows): f16
+    activations, epilogues bias / f16 store / residual add / SwiGLU on the small-M kernels
+    (quantized and f16 weights)."""
     check_forward_gemm(torch_cuda, t0hip, oracle, rng, qtype, 0, epi, m, k, n, sample=False)
 
 
