@@ -210,10 +210,16 @@ __device__ __forceinline__ void tile_bias1(const GemmDesc& d, int lane, int cbas
   b1 = (EPI == EPI_SWIGLU_F16 && ok) ? d.bias[d.N + col] : 0.0f;
 }
 
-template <int EPI, int TI, int TJ, bool PRE = false>
+// RN (split RMSNorm, see GemmDesc): 0 none; 1 consumer: rs holds the scale of
+// each of the tile's rows (rs[32 i + r] for row row_base + 32 i + r), applied to
+// the accumulators before the bias; 2 producer (EPI_RESID_F32, vector stores,
+// N % 32 == 0): the residual rows' f16 norm input and partial sums of squares.
+template <int EPI, int TI, int TJ, bool PRE = false, int RN = 0>
 __device__ __forceinline__ void store_tile(const GemmDesc& d, floatx16 (&acc)[TI][TJ], float* smemf, int wave,
                                            int lane, int row_base, int cbase, float pre0 = 0.0f,
-                                           float pre1 = 0.0f) {
+                                           float pre1 = 0.0f, const float* rs = nullptr) {
+  static_assert(RN != 1 || EPI != EPI_RESID_F32, "a residual epilogue is not a norm consumer");
+  static_assert(RN != 2 || EPI == EPI_RESID_F32, "only a residual epilogue produces the norm");
   constexpr bool SWI = EPI == EPI_SWIGLU_F16;
   static_assert(!PRE || TJ == 1, "a preloaded bias covers one column group");
   // SwiGLU with one column group (PAIR): lanes l%32 < 16 hold the gate and
@@ -225,6 +231,13 @@ __device__ __forceinline__ void store_tile(const GemmDesc& d, floatx16 (&acc)[TI
   const int M = d.M, N = d.N;
   float* stage = smemf + wave * 32 * SLD;
   const int lc = lane & 31, lr = (lane >> 5) * 4, uc = PAIR ? (lc & 15) : lc;
+  // row scale of accumulator element e of slice i (1 without a split RMSNorm)
+  auto rsc = [&](int i, int e) {
+    if constexpr (RN == 1)
+      return rs[i * 32 + (e >> 2) * 8 + lr + (e & 3)];
+    else
+      return 1.0f;
+  };
   float b0[NJ], b1[NJ];
   if constexpr (PRE) {
     b0[0] = pre0;
@@ -265,7 +278,8 @@ __device__ __forceinline__ void store_tile(const GemmDesc& d, floatx16 (&acc)[TI
           for (int k = 0; k < 8; ++k) {
             const auto gu = __builtin_amdgcn_permlane16_swap(__float_as_uint(acc[i][0][2 * k]),
                                                              __float_as_uint(acc[i][0][2 * k + 1]), false, false);
-            v[k] = silu(__uint_as_float(gu[0]) + b0[0]) * (__uint_as_float(gu[1]) + b1[0]);
+            const float sc = rsc(i, 2 * k + (lc >> 4));
+            v[k] = silu(__uint_as_float(gu[0]) * sc + b0[0]) * (__uint_as_float(gu[1]) * sc + b1[0]);
           }
 #pragma unroll
           for (int k = 0; k < 8; ++k) {
@@ -278,7 +292,7 @@ __device__ __forceinline__ void store_tile(const GemmDesc& d, floatx16 (&acc)[TI
         } else {
 #pragma unroll
           for (int e = 0; e < 16; ++e) {
-            float v = acc[i][0][e] + b0[0];
+            float v = acc[i][0][e] * rsc(i, e) + b0[0];
             if (d.relu) v = fmaxf(v, 0.0f);
             const float nb = dpp_move<0xB1>(v);  // lane l^1
             if ((e & 1) == odd) st[((e >> 2) * 8 + lr + (e & 3)) * SH + (lc >> 1)] = pack(v, nb);
@@ -329,18 +343,20 @@ __device__ __forceinline__ void store_tile(const GemmDesc& d, floatx16 (&acc)[TI
       for (int e = 0; e < 16; e += 2) {
         const auto gu = __builtin_amdgcn_permlane16_swap(__float_as_uint(acc[i][0][e]),
                                                          __float_as_uint(acc[i][0][e + 1]), false, false);
-        const float v = silu(__uint_as_float(gu[0]) + b0[0]) * (__uint_as_float(gu[1]) + b1[0]);
         const int ee = e + (lc >> 4);
+        const float sc = rsc(i, ee);
+        const float v = silu(__uint_as_float(gu[0]) * sc + b0[0]) * (__uint_as_float(gu[1]) * sc + b1[0]);
         stage[((ee >> 2) * 8 + lr + (ee & 3)) * SLD + uc] = v;
       }
     } else {
 #pragma unroll
       for (int e = 0; e < 16; ++e) {
         const int r = (e >> 2) * 8 + lr + (e & 3);
+        const float sc = rsc(i, e);
 #pragma unroll
         for (int j = 0; j < NJ; ++j)
-          stage[r * SLD + j * 32 + lc] =
-              SWI ? silu(acc[i][j][e] + b0[j]) * (acc[i][j + TJ / 2][e] + b1[j]) : acc[i][j][e] + b0[j];
+          stage[r * SLD + j * 32 + lc] = SWI ? silu(acc[i][j][e] * sc + b0[j]) * (acc[i][j + TJ / 2][e] * sc + b1[j])
+                                             : acc[i][j][e] * sc + b0[j];
       }
     }
     const int row0 = row_base + i * 32;
@@ -362,8 +378,16 @@ __device__ __forceinline__ void store_tile(const GemmDesc& d, floatx16 (&acc)[TI
         }
         if constexpr (RES) {
           const float4 old = yo[RES2 ? (i & 1) : 0][t];
-          *reinterpret_cast<float4*>(static_cast<float*>(d.y) + o) =
-              make_float4(old.x + v.x, old.y + v.y, old.z + v.z, old.w + v.w);
+          const float4 nx = make_float4(old.x + v.x, old.y + v.y, old.z + v.z, old.w + v.w);
+          *reinterpret_cast<float4*>(static_cast<float*>(d.y) + o) = nx;
+          if constexpr (RN == 2) {  // split RMSNorm producer (N % 32 == 0: a 32-column group's 8 lanes are all here)
+            const float4 g4 = *reinterpret_cast<const float4*>(d.norm_g + col);
+            const half4 hn = {(_Float16)(nx.x * g4.x * RN_SCALE), (_Float16)(nx.y * g4.y * RN_SCALE),
+                              (_Float16)(nx.z * g4.z * RN_SCALE), (_Float16)(nx.w * g4.w * RN_SCALE)};
+            *reinterpret_cast<half4*>(d.norm_out + (size_t)row * N + col) = hn;
+            const float sq = lane_sum8((nx.x * nx.x + nx.y * nx.y) + (nx.z * nx.z + nx.w * nx.w));
+            if ((lane & 7) == 0) d.norm_ssq[(size_t)row * (N / 32) + col / 32] = sq;
+          }
         } else if (EPI == EPI_STORE_F32) {
           *reinterpret_cast<float4*>(static_cast<float*>(d.y) + o) = v;
         } else {
@@ -955,6 +979,26 @@ struct BfCfg {
   static constexpr int BN = 32 * NWV, NBUF = NWV == 8 ? 3 : 2, ABUF = BM * LDK, LDS = NBUF * ABUF * 2;
 };
 
+// Split RMSNorm consumer: the scale of rows m0 .. m0 + n - 1 (rows past M use row
+// M - 1) into dst, from each row's ssq_parts partial sums of squares summed in order.
+// A row's partials (ssq_parts <= RN_MAX_PARTS, a multiple of 4, 16-byte aligned rows)
+// are loaded with every 16-byte load issued before the first is summed.
+constexpr int RN_MAX_PARTS = 32;
+__device__ __forceinline__ void row_scales(const GemmDesc& d, int m0, int n, float* dst) {
+  for (int t = threadIdx.x; t < n; t += blockDim.x) {
+    const float4* p = reinterpret_cast<const float4*>(d.row_ssq + (size_t)min(m0 + t, d.M - 1) * d.ssq_parts);
+    float4 v[RN_MAX_PARTS / 4];
+#pragma unroll
+    for (int q = 0; q < RN_MAX_PARTS / 4; ++q)
+      if (4 * q < d.ssq_parts) v[q] = p[q];
+    float ss = 0.0f;
+#pragma unroll
+    for (int q = 0; q < RN_MAX_PARTS / 4; ++q)
+      if (4 * q < d.ssq_parts) ss = (((ss + v[q].x) + v[q].y) + v[q].z) + v[q].w;
+    dst[t] = 1.0f / (RN_SCALE * sqrtf(ss / (float)d.ssq_dim + 1e-8f));
+  }
+}
+
 typedef uint32_t u32x8 __attribute__((ext_vector_type(8)));
 // The dequantization sub-step (0..3) that follows MFMA i of a TI-MFMA slice, or -1.
 __host__ __device__ constexpr int dq_sub_at(int i, int TI) {
@@ -1094,6 +1138,7 @@ __global__ __launch_bounds__(64 * NWV) __attribute__((amdgpu_waves_per_eu(2, 2))
   // slower with it and load theirs in store_tile.
   constexpr bool PREB = EPI == EPI_RESID_F32;
   const int cbase = SWI ? tn * HB + wave * 16 : tn * BN + wave * 32;
+
   float pb0 = 0.0f, pb1 = 0.0f;
   if constexpr (PREB) tile_bias1<EPI>(d, lane, cbase, pb0, pb1);
 
@@ -1433,7 +1478,7 @@ __device__ __forceinline__ half8 dq_frag(const uint32_t* r, int c, int h) {
   return __builtin_bit_cast(half8, make_uint4(v[0], v[1], v[2], v[3]));
 }
 
-template <int WT, bool A32, int EPI, int TI, int KR, int TJ>
+template <int WT, bool A32, int EPI, int TI, int KR, int TJ, int RN>
 __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2))) void k_gemm_mid(const GemmDesc d) {
   constexpr bool SWI = EPI == EPI_SWIGLU_F16;
   constexpr int NWD = WT == T0H_Q8_0 ? 9 : 5, SWD = WT == T0H_Q8_0 ? 17 : 9;
@@ -1445,6 +1490,10 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2))) void k
   const int M = d.M, N = d.N, K = d.K, KT = K / 64;
   const int strips = (N + W - 1) / W;
   const int tn = blockIdx.x % strips, m0 = (blockIdx.x / strips) * (32 * TI);
+  // split RMSNorm consumer: row scales after the partial tiles and the staging
+  // (read by the epilogue waves after the barrier below)
+  float* const rsc_s = red + nw * TI * TJ * 16 * 64 + TI * 32 * (W + 4);
+  if constexpr (RN == 1) row_scales(d, m0, 32 * TI, rsc_s);
   // column group j of the tile: the lane's weight row (rows past N read row 0,
   // activation rows past M read row M-1: never stored)
   const int s0 = wave * KR;
@@ -1540,7 +1589,8 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2))) void k
         sum[0][j][4 * q + 3] += v.w;
       }
   // staging after the partials (other slices may still be reading them)
-  store_tile<EPI, 1, TJ>(d, sum, red + nw * TI * TJ * 16 * 64, wave, lane, m0 + 32 * wave, tn * W);
+  store_tile<EPI, 1, TJ, false, RN>(d, sum, red + nw * TI * TJ * 16 * 64, wave, lane, m0 + 32 * wave, tn * W,
+                                    0.0f, 0.0f, rsc_s + 32 * wave);
 }
 
 // ---------------------------------------------------------------------------
@@ -1703,6 +1753,7 @@ void check_hip(hipError_t e, const char* what) {
 
 template <int WT, bool A32, int EPI, bool K64, int TI, int TJ>
 void run_gemm(const GemmDesc& d, hipStream_t s) {
+  if (d.row_ssq || d.norm_out) throw Error(T0H_ERR_HIP, "internal: split RMSNorm on a kernel without it");
   using C = Tile<TI, TJ>;
   const int hb = EPI == EPI_SWIGLU_F16 ? C::BN / 2 : C::BN;
   const int tiles_n = (d.N + hb - 1) / hb;
@@ -1722,6 +1773,7 @@ bool dma_ok(const GemmDesc& d) { return d.K % 128 == 0 && d.N % 4 == 0 && d.ldy 
 
 template <int WT, int EPI>
 void run_gemm_dma(const GemmDesc& d, hipStream_t s) {
+  if (d.row_ssq || d.norm_out) throw Error(T0H_ERR_HIP, "internal: split RMSNorm on a kernel without it");
   const int hb = EPI == EPI_SWIGLU_F16 ? DM_BN / 2 : DM_BN;
   const int tiles_n = (d.N + hb - 1) / hb;
   const int tiles_m = (d.M + DM_BM - 1) / DM_BM;
@@ -1733,6 +1785,7 @@ void run_gemm_dma(const GemmDesc& d, hipStream_t s) {
 
 template <int WT, int EPI, int NWV, bool A32 = false, int BM = BF_BM>
 void run_gemm_bf(const GemmDesc& d, hipStream_t s) {
+  if (d.row_ssq || d.norm_out) throw Error(T0H_ERR_HIP, "internal: split RMSNorm on a kernel without it");
   using C = BfCfg<NWV, BM>;
   const int hb = EPI == EPI_SWIGLU_F16 ? C::BN / 2 : C::BN;
   const int n_tiles = ((d.N + hb - 1) / hb) * ((d.M + BM - 1) / BM);
@@ -1928,6 +1981,7 @@ __global__ __launch_bounds__(64 * MF_WAVES) void k_gemv_mf(const GemmDesc d) {
 
 template <int WT, bool A32, int EPI>
 void run_gemv_mf(const GemmDesc& d, hipStream_t s) {
+  if (d.row_ssq || d.norm_out) throw Error(T0H_ERR_HIP, "internal: split RMSNorm on a kernel without it");
   const int per = EPI == EPI_SWIGLU_F16 ? 8 : 16;
   hipLaunchKernelGGL((k_gemv_mf<WT, A32, EPI>), dim3((d.N + per - 1) / per), dim3(64 * MF_WAVES), 0, s, d);
   check_hip(hipGetLastError(), "k_gemv_mf launch");
@@ -1944,6 +1998,7 @@ bool gemv_mf_ok(const GemmDesc& d) {
 
 template <int WT, bool A32, int EPI, int MT>
 void run_gemv(const GemmDesc& d, hipStream_t s) {
+  if (d.row_ssq || d.norm_out) throw Error(T0H_ERR_HIP, "internal: split RMSNorm on a kernel without it");
   const size_t rb = WT == T0H_F16 ? (size_t)d.K * 2 : (size_t)(d.K / 32) * block_bytes(WT);
   const size_t lds = std::max<size_t>(GV_NR * rb, 5 * GV_NR * MT * sizeof(float));
   const int seg_rows = EPI == EPI_SWIGLU_F16 ? GV_NR / 2 : GV_NR;
@@ -1957,6 +2012,7 @@ void run_gemv(const GemmDesc& d, hipStream_t s) {
 
 template <int WT, bool A32, int EPI, int MT, int NP>
 void run_gemv_s(const GemmDesc& d, hipStream_t s) {
+  if (d.row_ssq || d.norm_out) throw Error(T0H_ERR_HIP, "internal: split RMSNorm on a kernel without it");
   const size_t lds = (size_t)MT * GS_XS * sizeof(float);
   const int per = EPI == EPI_SWIGLU_F16 ? GS_NR / 2 : GS_NR;
   static std::atomic<uint64_t> lds_set{0};  // per instantiation
@@ -1998,18 +2054,37 @@ void dispatch_gemv(const GemmDesc& d, hipStream_t s) {
 // Waves of KR steps over K (at most 8 per workgroup, two per SIMD, so a wave
 // may hold its KR steps of operands: up to 256 registers); lds: the partial
 // tiles and the epilogue staging of TI waves.
-template <int WT, bool A32, int EPI, int TI, int KR, int TJ = 1>
-void run_gemm_mid(const GemmDesc& d, hipStream_t s) {
+template <int WT, bool A32, int EPI, int TI, int KR, int TJ, int RN>
+void launch_gemm_mid(const GemmDesc& d, hipStream_t s) {
   // at least one wave per 32-row slice: slice i is summed and stored by wave i
   const int KT = d.K / 64, nw = std::max(TI, (KT + KR - 1) / KR);
   if (nw > 8) throw Error(T0H_ERR_UNSUPPORTED, "gemm: K too large for the medium-M kernel");
   const int W = EPI == EPI_SWIGLU_F16 ? 16 : 32 * TJ;
-  const size_t lds = (size_t)nw * TI * TJ * 16 * 64 * 4 + (size_t)TI * 32 * (W + 4) * 4;
+  const size_t lds = (size_t)nw * TI * TJ * 16 * 64 * 4 + (size_t)TI * 32 * (W + 4) * 4 + (RN == 1 ? TI * 32 * 4 : 0);
   const int strips = (d.N + W - 1) / W, mt = (d.M + 32 * TI - 1) / (32 * TI);
   static std::atomic<uint64_t> lds_set{0};  // per instantiation
-  allow_dynamic_lds(reinterpret_cast<const void*>(&k_gemm_mid<WT, A32, EPI, TI, KR, TJ>), lds_set);
-  hipLaunchKernelGGL((k_gemm_mid<WT, A32, EPI, TI, KR, TJ>), dim3(strips * mt), dim3(64 * nw), lds, s, d);
+  allow_dynamic_lds(reinterpret_cast<const void*>(&k_gemm_mid<WT, A32, EPI, TI, KR, TJ, RN>), lds_set);
+  hipLaunchKernelGGL((k_gemm_mid<WT, A32, EPI, TI, KR, TJ, RN>), dim3(strips * mt), dim3(64 * nw), lds, s, d);
   check_hip(hipGetLastError(), "k_gemm_mid launch");
+}
+
+// The split RMSNorm roles (GemmDesc) are instantiations of their own: a consumer
+// is an f16-store or SwiGLU GEMM, a producer a residual one.
+template <int WT, bool A32, int EPI, int TI, int KR, int TJ = 1>
+void run_gemm_mid(const GemmDesc& d, hipStream_t s) {
+  if constexpr (EPI == EPI_RESID_F32) {
+    if (d.row_ssq) throw Error(T0H_ERR_HIP, "internal: a residual GEMM cannot consume the split RMSNorm");
+    if (d.norm_out) {
+      if (d.N % 32 || d.ldy % 4) throw Error(T0H_ERR_HIP, "internal: split RMSNorm producer needs N % 32 == 0");
+      return launch_gemm_mid<WT, A32, EPI, TI, KR, TJ, 2>(d, s);
+    }
+  } else {
+    if (d.norm_out) throw Error(T0H_ERR_HIP, "internal: only a residual GEMM produces the split RMSNorm");
+    if constexpr (!A32 && (EPI == EPI_STORE_F16 || EPI == EPI_SWIGLU_F16))
+      if (d.row_ssq) return launch_gemm_mid<WT, A32, EPI, TI, KR, TJ, 1>(d, s);
+    if (d.row_ssq) throw Error(T0H_ERR_HIP, "internal: split RMSNorm consumer on an unsupported epilogue");
+  }
+  launch_gemm_mid<WT, A32, EPI, TI, KR, TJ, 0>(d, s);
 }
 
 // Compute units of the current device (the round size of a launch).
@@ -2101,6 +2176,24 @@ void dispatch_type(const GemmDesc& d, int force, hipStream_t s) {
 }
 
 }  // namespace
+
+// Mirrors the automatic choice (force 0) of dispatch_w: only the medium-M kernel
+// (quantized weights, f16 activations, K % 64 == 0, 16 < M < 1024 up to
+// MID_MN_MAX outputs) has the split RMSNorm epilogues.
+namespace {
+bool mid_auto(const GemmDesc& d) {
+  return d.wtype != T0H_F16 && !d.a_f32 && d.M > 16 && d.M < MID_M_MAX && (long long)d.M * d.N <= MID_MN_MAX &&
+         mid_ok(d);
+}
+}  // namespace
+bool rownorm_producer_ok(const GemmDesc& d) {
+  return d.epi == EPI_RESID_F32 && mid_auto(d) && d.N % 32 == 0 && d.ldy % 4 == 0 && !d.row_add;
+}
+bool rownorm_consumer_ok(const GemmDesc& d) {
+  if (d.epi != EPI_STORE_F16 && d.epi != EPI_SWIGLU_F16) return false;
+  if (d.ssq_parts % 4 || d.ssq_parts > RN_MAX_PARTS) return false;
+  return mid_auto(d);
+}
 
 void launch_gemm_forced(const GemmDesc& d, int force, hipStream_t s) {
   if (d.M <= 0 || d.N <= 0) return;

@@ -46,7 +46,24 @@ struct GemmDesc {
   const float* row_add = nullptr;  // EPI_STORE_F32 only: [n_rows_table, N]
   const int* row_add_idx = nullptr;
   int epi = EPI_STORE_F32;
+  // RMSNorm split across two GEMMs (rownorm_producer_ok / rownorm_consumer_ok).
+  // Producer (EPI_RESID_F32): besides the new residual rows x, writes
+  // norm_out[m, n] = f16(x[m, n] * norm_g[n] * RN_SCALE) (row stride N) and
+  // norm_ssq[m, n / 32] = sum of x[m, n]^2 over each 32-column group.
+  const float* norm_g = nullptr;
+  _Float16* norm_out = nullptr;
+  float* norm_ssq = nullptr;
+  // Consumer (activations = a producer's norm_out): every output row is scaled
+  // by 1 / (RN_SCALE * sqrt(sum of its ssq_parts partials / ssq_dim + 1e-8))
+  // before the bias, which makes it the GEMM of the RMSNorm'd rows
+  // (ops.rs:12-17: x / sqrt(mean(x^2) + eps) * scale).
+  const float* row_ssq = nullptr;
+  int ssq_parts = 0, ssq_dim = 0;
 };
+constexpr float RN_SCALE = 0.0625f;  // keeps unnormalized rows 16x further from the f16 range limit
+// Whether the kernel launch_gemm picks for `d` can produce / consume the split RMSNorm.
+bool rownorm_producer_ok(const GemmDesc& d);
+bool rownorm_consumer_ok(const GemmDesc& d);
 
 void launch_gemm(const GemmDesc& d, hipStream_t s);
 // force = 0: pick by shape (M <= 16 small-M kernels; 16 < M < 1024 the split-K

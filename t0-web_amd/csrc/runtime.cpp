@@ -608,6 +608,48 @@ void encode_and_layers(t0h_model* m, int v, int p, const PatchMeta& pm, float* t
   const int* seg_len = ws_get<int>(m, "seg_len", v);
   if (!m->ws.arena.on && m->ws.rope_p != p) throw Error(T0H_ERR_HIP, "internal: RoPE tables not prepared for this window");
 
+  // RMSNorm split across the GEMMs either side of it (ops.rs:12-17): each residual
+  // GEMM of the layers (wO, w2) also writes f16(x * g / 16) and per-row
+  // partial sums of squares, and the consuming GEMM (QKV, SwiGLU) scales its output
+  // rows by 16 / sqrt(mean + eps).  Used below 1024 rows when every kernel involved
+  // supports it (one series, config 3: 0.597 -> 0.582 ms: 23 fewer launches); at
+  // config 4 it measured 5 % slower (the producers' epilogues +40 us, the consumers'
+  // per-tile wait for their rows' sums +24 us, against 68 us of norm launches per
+  // layer), so larger windows keep each norm as its own launch.
+  _Float16* xnorm = nullptr;
+  float* ssq = nullptr;
+  bool split = false;
+  if (!m->layers.empty() && M < 1024) {
+    const Layer& L0 = m->layers[0];
+    GemmDesc q = gemm(L0.qkv, xn, E, L0.b_qkv, qkv, 3 * E, M, EPI_STORE_F16);
+    GemmDesc w0 = gemm(L0.w0, xn, E, L0.b0, hb, H, M, EPI_SWIGLU_F16);
+    GemmDesc res = gemm(L0.o, xn, E, L0.b_o, x, E, M, EPI_RESID_F32);
+    GemmDesc res2 = gemm(L0.w2, hb, H, L0.b2, x, E, M, EPI_RESID_F32);
+    q.ssq_parts = w0.ssq_parts = E / 32;
+    split = rownorm_consumer_ok(q) && rownorm_consumer_ok(w0) && rownorm_producer_ok(res) &&
+            rownorm_producer_ok(res2);
+    for (size_t li = 1; li < m->layers.size() && split; ++li)  // every layer's weights alike
+      split = m->layers[li].qkv.type == L0.qkv.type && m->layers[li].w0.type == L0.w0.type;
+  }
+  if (split) {
+    xnorm = ws_get<_Float16>(m, "xnorm", (size_t)M * E);
+    ssq = ws_get<float>(m, "ssq", (size_t)M * (E / 32));
+  }
+  auto produce = [&](GemmDesc& g, const float* scale) {  // the next norm, into xnorm / ssq
+    if (!split || !scale) return;
+    g.norm_g = scale;
+    g.norm_out = xnorm;
+    g.norm_ssq = ssq;
+  };
+  auto consume = [&](GemmDesc& g) {
+    if (!split) return;
+    g.a = xnorm;
+    g.lda = E;
+    g.row_ssq = ssq;
+    g.ssq_parts = E / 32;
+    g.ssq_dim = E;
+  };
+
   // patch encoder residual block + type embedding (model.rs:199-207)
   {
     ProfScope ps_(m, "gemm_encoder");
@@ -637,13 +679,15 @@ void encode_and_layers(t0h_model* m, int v, int p, const PatchMeta& pm, float* t
   ad.seg_max = m->ws.seg_max;
   for (size_t li = 0; li < m->layers.size(); ++li) {
     const Layer& L = m->layers[li];
-    {
+    if (!split || li == 0) {  // the encoder's output (F16 weights) has no split epilogue
       ProfScope ps_(m, "rmsnorm");
       launch_rmsnorm(x, L.norm, xn, nullptr, M, E, s);
     }
     {
       ProfScope ps_(m, "gemm_qkv");
-      launch_gemm(gemm(L.qkv, xn, E, L.b_qkv, qkv, 3 * E, M, EPI_STORE_F16), s);
+      GemmDesc g = gemm(L.qkv, xn, E, L.b_qkv, qkv, 3 * E, M, EPI_STORE_F16);
+      if (li > 0) consume(g);
+      launch_gemm(g, s);
     }
     ad.q_norm = L.q_norm;
     ad.k_norm = L.k_norm;
@@ -658,19 +702,25 @@ void encode_and_layers(t0h_model* m, int v, int p, const PatchMeta& pm, float* t
     }
     {
       ProfScope ps_(m, "gemm_wo_resid");
-      launch_gemm(gemm(L.o, xn, E, L.b_o, x, E, M, EPI_RESID_F32), s);
+      GemmDesc g = gemm(L.o, xn, E, L.b_o, x, E, M, EPI_RESID_F32);
+      produce(g, L.mlp_norm);
+      launch_gemm(g, s);
     }
-    {
+    if (!split) {
       ProfScope ps_(m, "rmsnorm");
       launch_rmsnorm(x, L.mlp_norm, xn, nullptr, M, E, s);
     }
     {
       ProfScope ps_(m, "gemm_w0_swiglu");
-      launch_gemm(gemm(L.w0, xn, E, L.b0, hb, H, M, EPI_SWIGLU_F16), s);
+      GemmDesc g = gemm(L.w0, xn, E, L.b0, hb, H, M, EPI_SWIGLU_F16);
+      consume(g);
+      launch_gemm(g, s);
     }
     {
       ProfScope ps_(m, "gemm_w2_resid");
-      launch_gemm(gemm(L.w2, hb, H, L.b2, x, E, M, EPI_RESID_F32), s);
+      GemmDesc g = gemm(L.w2, hb, H, L.b2, x, E, M, EPI_RESID_F32);
+      produce(g, li + 1 < m->layers.size() ? m->layers[li + 1].norm : nullptr);  // out_norm stays a launch
+      launch_gemm(g, s);
     }
     if (li == 0 && trace_l0) download(m, trace_l0, x, (size_t)M * E);
   }
@@ -702,6 +752,8 @@ void reserve_forward(t0h_model* m, int rows, int dec_rows) {
   ws_get<_Float16>(m, "xn", M * wide);
   ws_get<_Float16>(m, "qkv", M * 3 * E);
   ws_get<_Float16>(m, "h", M * c.mlp_hidden_dim);
+  ws_get<_Float16>(m, "xnorm", M * E);  // the split RMSNorm's rows and partial sums (if used)
+  ws_get<float>(m, "ssq", M * (E / 32));
   ws_get<_Float16>(m, "dec_in", (size_t)dec_rows * E);
   ws_get<_Float16>(m, "dec_h", (size_t)dec_rows * m->dec.hid.n);
   ws_get<float>(m, "dec_out", (size_t)dec_rows * m->dec.out.n);
