@@ -231,9 +231,10 @@ def cpu_baseline(gguf, x, groups, t_ctx, horizon, budget_s=12.0):
 # Device kernel behind each profiled GEMM kind of the forward at config 4
 # (template args: weight type 2 = Q4_0 / 8 = Q8_0, epilogue 1 f16 store / 3 SwiGLU,
 # waves, f32 activations).
-KERNEL_OF = {("gemm_w0_swiglu", "q4_0"): "k_gemm_bf<2, 3, 4, false>",
-             ("gemm_w0_swiglu", "q8_0"): "k_gemm_bf<8, 3, 4, false>",
-             ("gemm_qkv", "q4_0"): "k_gemm_bf<2, 1, 4, false>", ("gemm_qkv", "q8_0"): "k_gemm_bf<8, 1, 4, false>"}
+KERNEL_OF = {("gemm_w0_swiglu", "q4_0"): "k_gemm_bf<2, 3, 4, false, 256>",
+             ("gemm_w0_swiglu", "q8_0"): "k_gemm_bf<8, 3, 4, false, 256>",
+             ("gemm_qkv", "q4_0"): "k_gemm_bf<2, 1, 4, false, 256>",
+             ("gemm_qkv", "q8_0"): "k_gemm_bf<8, 1, 4, false, 256>"}
 COPY_BYTES = 256 << 20  # the --calibrate-copy kernel reads and writes this many bytes
 TRAFFIC_FILE = os.path.join(ROOT, "profiles", "traffic_config4.json")
 
@@ -297,7 +298,46 @@ def summarize(prof_dir, fetch_dir, write_dir, quant, kind):
     return "\n".join(lines), res
 
 
+def trace_table(trace_dir, min_calls=1):
+    """Per (kernel, grid) median / mean duration from a rocprofv3 --kernel-trace csv directory,
+    in first-dispatch order: consecutive launches of one shape (the GEMM sweep, a forecast's
+    kernel sequence) each get a row."""
+    import csv
+    import glob
+    import re
+    files = glob.glob(os.path.join(trace_dir, "**", "*kernel_trace.csv"), recursive=True)
+    if not files:
+        raise SystemExit(f"{trace_dir}: no kernel_trace.csv")
+    rows = list(csv.DictReader(open(files[0])))
+    rows.sort(key=lambda r: int(r["Start_Timestamp"]))
+    groups, order = {}, []
+    for r in rows:
+        name = re.sub(r"\(t0h::\w+(, t0h::\w+)?\)$|\(.*\)$", "", r["Kernel_Name"].replace("(anonymous namespace)::", ""))
+        name = name.replace("void ", "").replace("t0h::", "")
+        key = (name, int(r["Grid_Size_X"]), int(r["Workgroup_Size_X"]))
+        if key not in groups:
+            groups[key] = []
+            order.append(key)
+        groups[key].append(int(r["End_Timestamp"]) - int(r["Start_Timestamp"]))
+    lines = ["| kernel | workgroups x threads | calls | median us | mean us |", "|---|---|---|---|---|"]
+    for key in order:
+        d = groups[key]
+        if len(d) < min_calls:
+            continue
+        d.sort()
+        lines.append(f"| `{key[0][:100]}` | {key[1] // max(key[2], 1)} x {key[2]} | {len(d)} | {d[len(d) // 2] / 1e3:.2f} | "
+                     f"{sum(d) / len(d) / 1e3:.2f} |")
+    return "\n".join(lines)
+
+
 def main():
+    if len(sys.argv) > 1 and sys.argv[1] == "--trace-table":
+        sp = argparse.ArgumentParser()
+        sp.add_argument("--trace-table", metavar="TRACE_DIR", required=True)
+        sp.add_argument("--min-calls", type=int, default=1)
+        a = sp.parse_args()
+        print(trace_table(a.trace_table, a.min_calls))
+        return
     if len(sys.argv) > 1 and sys.argv[1] == "--summarize":
         sp = argparse.ArgumentParser()
         sp.add_argument("--summarize", nargs=3, metavar=("PROF_DIR", "FETCH_DIR", "WRITE_DIR"), required=True)
