@@ -31,7 +31,9 @@ extern "C" {
 #define T0H_ABI_VERSION 1
 #define T0H_MAX_QUANTILES 64
 #define T0H_MAX_HORIZON 1024 /* crates/t0-core/src/model.rs:26 MAX_HORIZON */
-#define T0H_MAX_PATCHES 256  /* time-attention window per forward, in patches */
+/* Longest window of t0h_forecast_grouped_dev_noalloc, in patches (the other entry
+   points take any window that fits in device memory, like t0-core). */
+#define T0H_NOALLOC_MAX_PATCHES 256
 /* Device scratch of t0h_forecast_grouped_dev_noalloc, one per GPU (32 MiB). */
 #define T0H_NOALLOC_SCRATCH_BYTES (32u << 20)
 
@@ -55,6 +57,9 @@ enum t0h_status {
   T0H_ERR_OOM = -15,             /* host or device allocation failed */
   T0H_ERR_SAFETENSORS = -16,     /* weights.rs:123-129 bad safetensors file or a non-F32 tensor */
   T0H_ERR_CONFIG = -17,          /* main.rs:285 config.json not a T0Config (serde_json error) */
+  T0H_ERR_NUMERIC = -18,         /* no reference counterpart: a forecast's model outputs are not finite
+                                    (an f16 activation beyond +-65504, or non-finite weights); the
+                                    reference's f32 path would return them without an error */
 };
 
 /* ggml tensor type ids (gguf.rs:31-49) */
@@ -141,6 +146,17 @@ int t0h_model_profile_entry(t0h_model* model, size_t i, char* name, size_t name_
  * that; off (enable = 0) every window runs eagerly.  Results are identical
  * either way.  While the profiler records events, windows run eagerly. */
 int t0h_model_graph_replay(t0h_model* model, int enable);
+
+/* Numeric guard (no counterpart in the reference, whose activations are f32).
+ * The forward keeps its activations between kernels in f16; a value beyond
+ * +-65504 there becomes inf and the forecast's outputs NaN.  Every forecast
+ * records on the device whether any quantile logit was not finite.  The
+ * host-output forecast entry points read that record with their results and
+ * return T0H_ERR_NUMERIC (with the outputs written) when it is set; the
+ * device-output ones (t0h_forecast_grouped_dev, _noalloc) do not wait, and
+ * this call waits for the model's stream, returns T0H_ERR_NUMERIC if any
+ * forecast since the last read was not finite, and clears the record. */
+int t0h_model_check_numerics(t0h_model* model);
 
 /* ---- forward ----------------------------------------------------------- */
 /* ≡ model::forward_async (t0-fast model.rs:693-808) ≡ T0Model::forward (t0-core

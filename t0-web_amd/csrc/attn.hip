@@ -299,6 +299,193 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(MAXKT <= 8 
   }
 }
 
+// Windows longer than the LDS kernel holds (T0H_LDS_PATCHES): the keys after
+// QK-norm + RoPE and the values, transposed, are written once to workspace,
+// then every wave streams them for one 16-query tile in 32-key chunks with an
+// online softmax (running max and sum per query).
+//
+// k_time_kprep: one workgroup per (row, head, 32-key chunk).  Layouts (P32 =
+// p rounded up to 32; keys >= p zero):
+//   kr [row][head][P32][64]  keys, normalized and rotated as k_time_attn does
+//   vt [row][head][64][P32]  values by dimension
+//   kg [row][P32]            key group if attendable, -2 if not, -4 past p
+__global__ __launch_bounds__(256) void k_time_kprep(const AttnDesc d) {
+  __shared__ _Float16 vs[32][HD + 8];
+  const int p = d.p, P32 = round_up(p, 32), nch = P32 / 32, E = d.E, ld = 3 * E;
+  const int ch = blockIdx.x % nch, rh = blockIdx.x / nch, r = rh / d.heads, h = rh % d.heads;
+  const int tid = threadIdx.x, kl = tid >> 3, d0 = (tid & 7) * 8, i = ch * 32 + kl;
+  const size_t row0 = (size_t)r * p;
+  const _Float16* qb = d.qkv + row0 * ld + h * HD;
+  uint4 kx = make_uint4(0, 0, 0, 0), vx = make_uint4(0, 0, 0, 0);
+  if (i < p) {
+    kx = *reinterpret_cast<const uint4*>(qb + E + (size_t)i * ld + d0);
+    vx = *reinterpret_cast<const uint4*>(qb + 2 * E + (size_t)i * ld + d0);
+  }
+  float x[8];
+  unpack8(kx, x);
+  float ss = 0.0f;
+#pragma unroll
+  for (int e = 0; e < 8; ++e) ss += x[e] * x[e];
+  ss = lane_sum8(ss);
+  half8 o = {};
+  if (i < p) {
+    float a[8], b[8];
+    load_f8(d.rope_k + (size_t)i * 128 + d0, a);
+    load_f8(d.rope_k + (size_t)i * 128 + 64 + d0, b);
+    o = rotate8(x, a, b, 1.0f / sqrtf(ss / (float)HD + 1e-8f));
+  }
+  *reinterpret_cast<uint4*>(d.kr + ((size_t)rh * P32 + i) * HD + d0) = __builtin_bit_cast(uint4, o);
+  *reinterpret_cast<uint4*>(&vs[kl][d0]) = vx;
+  if (h == 0 && tid < 32) {
+    const int j = ch * 32 + tid;
+    d.kg[(size_t)r * P32 + j] = j >= p ? -4 : d.att[row0 + j] ? d.grp[row0 + j] : -2;
+  }
+  __syncthreads();
+  const int dim = tid >> 2, k8 = (tid & 3) * 8;
+  half8 w;
+#pragma unroll
+  for (int j = 0; j < 8; ++j) w[j] = vs[k8 + j][dim];
+  *reinterpret_cast<uint4*>(d.vt + ((size_t)rh * HD + dim) * P32 + ch * 32 + k8) = __builtin_bit_cast(uint4, w);
+}
+
+// k_time_attn_long: four waves per workgroup, one 16-query tile each, four
+// consecutive tiles of one (row, head) per workgroup (they read the same keys).
+// Per 32-key chunk: S^T = K Q^T on two 16-key tiles (lane: query lane%16, keys
+// 4(lane/16)..+3 of each tile), the mask, the running max and sum of the
+// query's scores, and O^T += V^T P^T, so each lane's output column is its own
+// query and the rescale by exp(old max - new max) needs no lane exchange.  The
+// next chunk's keys and values are loaded while the current one is computed.
+// Mask and blocked-query semantics are k_time_attn's.
+__global__ __launch_bounds__(256) void k_time_attn_long(const AttnDesc d) {
+  const int p = d.p, P32 = round_up(p, 32), nqt = round_up(p, 16) / 16, quads = (nqt + 3) / 4;
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6, part = lane >> 4;
+  const int rh = blockIdx.x / quads, qt = (blockIdx.x % quads) * 4 + wave;
+  if (qt >= nqt) return;  // whole waves; no barrier below
+  const int r = rh / d.heads, h = rh % d.heads;
+  const int E = d.E, ld = 3 * E;
+  const size_t row0 = (size_t)r * p;
+  const int qi = qt * 16 + (lane & 15);
+  const _Float16* kr = d.kr + (size_t)rh * P32 * HD;
+  const _Float16* vt = d.vt + (size_t)rh * HD * P32;
+  const int* kgr = d.kg + (size_t)r * P32;
+
+  // the tile's queries, normalized and rotated into the B operand layout
+  half8 bq0 = {}, bq1 = {};
+  {
+    uint4 qa = make_uint4(0, 0, 0, 0), qc = make_uint4(0, 0, 0, 0);
+    float ta[16], tb[16];
+    if (qi < p) {
+      const _Float16* qrow = d.qkv + (row0 + qi) * ld + h * HD;
+      qa = *reinterpret_cast<const uint4*>(qrow + part * 8);
+      qc = *reinterpret_cast<const uint4*>(qrow + 32 + part * 8);
+      const float* t = d.rope_q + (size_t)qi * 128 + part * 8;
+      load_f8(t, ta);
+      load_f8(t + 32, ta + 8);
+      load_f8(t + 64, tb);
+      load_f8(t + 96, tb + 8);
+    }
+    float x[16];
+    unpack8(qa, x);
+    unpack8(qc, x + 8);
+    float ss = 0.0f;
+#pragma unroll
+    for (int e = 0; e < 16; ++e) ss += x[e] * x[e];
+    ss = rows_sum(ss);  // the four lanes holding the query (all lanes take part)
+    if (qi < p) {
+      const float inv = 1.0f / sqrtf(ss / (float)HD + 1e-8f);
+      bq0 = rotate8(x, ta, tb, inv);
+      bq1 = rotate8(x + 8, ta + 8, tb + 8, inv);
+    }
+  }
+  const int kq = qi < p ? kgr[qi] : -4;
+  const bool fut = d.fut[r] != 0, blocked = kq < 0;
+  const bool need_all = fut || __ballot(qi < p && blocked) != 0;
+  const int nch = need_all ? P32 / 32 : min(P32 / 32, (qt * 16 + 16 + 31) / 32);
+
+  struct Chunk {
+    uint4 k[2][2];  // two 16-key tiles x (dims part*8, 32 + part*8)
+    uint2 v[4][2];  // per 16-dim tile: keys 4part..+3 and 16 + 4part..+3
+    int4 g[2];      // key groups of the lane's keys in each tile
+  };
+  auto load_chunk = [&](int c, Chunk& ck) {
+#pragma unroll
+    for (int t = 0; t < 2; ++t) {
+      const _Float16* krow = kr + (size_t)(32 * c + 16 * t + (lane & 15)) * HD + part * 8;
+      ck.k[t][0] = *reinterpret_cast<const uint4*>(krow);
+      ck.k[t][1] = *reinterpret_cast<const uint4*>(krow + 32);
+      ck.g[t] = *reinterpret_cast<const int4*>(kgr + 32 * c + 16 * t + part * 4);
+    }
+#pragma unroll
+    for (int dt = 0; dt < 4; ++dt) {
+      const _Float16* vrow = vt + (size_t)(dt * 16 + (lane & 15)) * P32 + 32 * c + part * 4;
+      ck.v[dt][0] = *reinterpret_cast<const uint2*>(vrow);
+      ck.v[dt][1] = *reinterpret_cast<const uint2*>(vrow + 16);
+    }
+  };
+
+  floatx4 o[4];
+#pragma unroll
+  for (int dt = 0; dt < 4; ++dt) o[dt] = (floatx4){0.f, 0.f, 0.f, 0.f};
+  float mrun = -INFINITY, lsum = 0.0f;
+  Chunk cur;
+  load_chunk(0, cur);
+  Chunk nxt = cur;
+  for (int c = 0; c < nch; ++c) {
+    if (c + 1 < nch) load_chunk(c + 1, nxt);
+    float sc[2][4];
+    float mc = -INFINITY;
+#pragma unroll
+    for (int t = 0; t < 2; ++t) {
+      floatx4 s = {0.f, 0.f, 0.f, 0.f};
+      s = __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(half8, cur.k[t][0]), bq0, s, 0, 0, 0);
+      s = __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(half8, cur.k[t][1]), bq1, s, 0, 0, 0);
+      const int kgv[4] = {cur.g[t].x, cur.g[t].y, cur.g[t].z, cur.g[t].w};
+      const int key0 = 32 * c + 16 * t + part * 4;
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        const bool ok = kgv[e] == kq && (fut || key0 + e <= qi);
+        sc[t][e] = blocked ? (kgv[e] != -4 ? 0.0f : -INFINITY) : ok ? s[e] * 0.125f : -INFINITY;
+        mc = fmaxf(mc, sc[t][e]);
+      }
+    }
+    mc = rows_max(mc);
+    const float mnew = fmaxf(mrun, mc);
+    const float mref = mnew == -INFINITY ? 0.0f : mnew;  // nothing attended yet: keep zeros
+    const float alpha = __expf(mrun - mref);
+    mrun = mnew;
+    half8 pb;
+    float ls = 0.0f;
+#pragma unroll
+    for (int t = 0; t < 2; ++t)
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        const float w = __expf(sc[t][e] - mref);
+        ls += w;
+        pb[4 * t + e] = (_Float16)w;
+      }
+    lsum = lsum * alpha + ls;
+#pragma unroll
+    for (int dt = 0; dt < 4; ++dt) {
+#pragma unroll
+      for (int e = 0; e < 4; ++e) o[dt][e] *= alpha;
+      const half4 lo = __builtin_bit_cast(half4, cur.v[dt][0]), hi = __builtin_bit_cast(half4, cur.v[dt][1]);
+      const half8 av = {lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
+      o[dt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(av, pb, o[dt], 0, 0, 0);
+    }
+    cur = nxt;
+  }
+  const float inv = 1.0f / rows_sum(lsum);
+  if (qi < p) {
+    _Float16* orow = d.out + (row0 + qi) * E + h * HD;
+#pragma unroll
+    for (int dt = 0; dt < 4; ++dt) {
+      const half4 w = {(_Float16)(o[dt][0] * inv), (_Float16)(o[dt][1] * inv), (_Float16)(o[dt][2] * inv),
+                       (_Float16)(o[dt][3] * inv)};
+      *reinterpret_cast<half4*>(orow + dt * 16 + part * 4) = w;
+    }
+  }
+}
+
 // Group attention: 8 lanes per (query row, head), each lane owning 8 of the
 // 64 dims; a wave covers 8 consecutive heads of a row, so every q/k/v load is
 // one contiguous 1 KB span.  Keys are the query row's group (a segment of the
@@ -504,10 +691,16 @@ void launch_time_attention(const AttnDesc& d, hipStream_t s) {
   if (d.v <= 0 || d.p <= 0) return;
   check_common(d);
   if (!d.att || !d.fut || !d.rope_q || !d.rope_k) throw Error(T0H_ERR_INVALID_ARG, "time attention: null pointer");
-  if (d.p > T0H_MAX_PATCHES)
-    throw Error(T0H_ERR_UNSUPPORTED, "time attention: window of " + std::to_string(d.p) + " patches exceeds " +
-                                         std::to_string(T0H_MAX_PATCHES));
-  static_assert(T0H_MAX_PATCHES <= 16 * 16, "the largest instance covers 16 key tiles of 16");
+  if (d.p > T0H_LDS_PATCHES) {
+    if (!d.kr || !d.vt || !d.kg) throw Error(T0H_ERR_INVALID_ARG, "time attention: long window without key workspace");
+    const int nch = round_up(d.p, 32) / 32, quads = (round_up(d.p, 16) / 16 + 3) / 4;
+    hipLaunchKernelGGL(k_time_kprep, dim3(d.v * d.heads * nch), dim3(256), 0, s, d);
+    check_hip(hipGetLastError(), "k_time_kprep launch");
+    hipLaunchKernelGGL(k_time_attn_long, dim3(d.v * d.heads * quads), dim3(256), 0, s, d);
+    check_hip(hipGetLastError(), "k_time_attn_long launch");
+    return;
+  }
+  static_assert(T0H_LDS_PATCHES <= 16 * 16, "the largest instance covers 16 key tiles of 16");
   const size_t lds = time_attn_lds(d.p);
   const int kt = round_up(d.p, 32) / 16;
   // Few (row, head) pairs (one or two series): split each one's query tiles over

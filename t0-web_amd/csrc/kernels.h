@@ -102,7 +102,16 @@ struct AttnDesc {
   const int* seg_len = nullptr;      // [v]
   int seg_max = 0;                   // longest segment (selects the kernel)
   int qsplit = 1;                    // time attention: workgroups per (row, head), set by the launcher
+  // time attention past T0H_LDS_PATCHES patches: workspace for the prepared keys
+  // [v][heads][P32][64], the transposed values [v][heads][64][P32] and the key
+  // groups [v][P32] (P32 = p rounded up to 32); null otherwise
+  _Float16* kr = nullptr;
+  _Float16* vt = nullptr;
+  int* kg = nullptr;
 };
+// Longest window the single-pass (LDS-resident keys) time attention takes; longer
+// windows stream their keys through workspace (AttnDesc kr / vt / kg).
+constexpr int T0H_LDS_PATCHES = 256;
 void launch_time_attention(const AttnDesc& d, hipStream_t s);
 void launch_group_attention(const AttnDesc& d, hipStream_t s);
 
@@ -118,7 +127,14 @@ struct WindowDesc {
   int v = 0, t_ctx = 0, horizon = 0, pad_left = 0, t = 0, ps = 0;
   int use_arcsinh = 1, variance_offset = 1;
   float eps = 0.1f;
+  // windows whose per-row arrays exceed the LDS: one prep_row_bytes(t, ps) area per
+  // row in device memory (null when the window fits the LDS)
+  uint8_t* rows_mem = nullptr;
 };
+// Bytes of one row's prep arrays (values, scaled values, per-patch loc / scale,
+// step masks), and whether they fit the LDS of one workgroup.
+size_t prep_row_bytes(int t, int ps);
+bool prep_fits_lds(int t, int ps);
 struct PatchOut {
   _Float16* enc_in = nullptr;  // [v*p, 3*ps]
   int* grp = nullptr;          // [v*p]
@@ -153,6 +169,7 @@ struct ForecastOutDesc {
   const float* patch_loc = nullptr;
   const float* patch_scale = nullptr;
   float* out = nullptr;  // [v, horizon, nq]
+  int* nonfinite = nullptr;  // set to 1 when a quantile logit is not finite (may be null)
   int v = 0, p = 0, ctx_p = 0, hp = 0, ps = 0, nq = 0, horizon = 0, use_arcsinh = 1;
 };
 void launch_forecast_out(const ForecastOutDesc& d, hipStream_t s);

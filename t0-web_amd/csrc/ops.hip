@@ -159,19 +159,26 @@ __device__ __forceinline__ Wf wf_merge(Wf a, Wf b) {
 // patch's loc/scale at its last step for the rescale (scaler.rs:125-148).
 // Each thread runs the reference's sequential Welford recurrence over its own
 // chunk of steps, starting from the merged state of all earlier chunks.
+__host__ __device__ inline size_t row_bytes(int t, int ps) {
+  return ((size_t)(2 * t + 2 * (t / ps)) * 4 + (size_t)t + 255) / 256 * 256;
+}
+
+// The row's arrays live in the LDS (GM false) or, for windows too long for it,
+// in the row's area of w.rows_mem (GM true); the same code runs on either.
+template <bool GM>
 __global__ __launch_bounds__(256) void k_prep_rows(const WindowDesc w, const PatchOut o) {
   extern __shared__ __align__(16) float psm[];
+  __shared__ Wf st[2 * 256];  // scan buffers
   const int t = w.t, ps = w.ps, p = t / ps, r = blockIdx.x, tid = threadIdx.x;
-  float* xs = psm;             // [t] VALID value, NaN otherwise
+  float* xs = GM ? reinterpret_cast<float*>(w.rows_mem + (size_t)r * row_bytes(t, ps)) : psm;  // [t] VALID value, NaN otherwise
   float* scv = xs + t;         // [t] scaled value
   float* pl = scv + t;         // [p] loc at patch end
   float* psc = pl + p;         // [p] scale at patch end
-  Wf* st = reinterpret_cast<Wf*>(psc + p);  // [2][256] scan buffers
   // [t] step masks: the later passes read them here instead of calling
   // window_step again (a dependent global load per step; one row's patch
   // metadata loop alone took about 20 us that way).  A step's group is the
   // row's and its type TARGET unless the step is PAD (group and type -1).
-  unsigned char* smask = reinterpret_cast<unsigned char*>(st + 2 * 256);
+  unsigned char* smask = reinterpret_cast<unsigned char*>(psc + p);
 
   for (int s = tid; s < t; s += 256) {
     const Step stp = window_step(w, r, s);
@@ -257,9 +264,12 @@ __global__ __launch_bounds__(256) void k_prep_rows(const WindowDesc w, const Pat
   }
 }
 
-size_t prep_lds(int t, int ps) {
-  return (size_t)(2 * t + 2 * (t / ps)) * 4 + 2 * 256 * sizeof(Wf) + (size_t)(t + 3) / 4 * 4;
-}
+}  // namespace
+
+size_t prep_row_bytes(int t, int ps) { return row_bytes(t, ps); }
+bool prep_fits_lds(int t, int ps) { return prep_row_bytes(t, ps) + 2 * 256 * sizeof(Wf) <= 160 * 1024; }
+
+namespace {
 
 __global__ __launch_bounds__(256) void k_series_patchify(const SeriesDev sd, const PatchOut o) {
   const int p = sd.t / sd.ps;
@@ -315,11 +325,14 @@ __global__ __launch_bounds__(256) void k_forecast_out(const ForecastOutDesc d) {
   const float* src = d.dec + (size_t)rh * d.ps * d.nq + (size_t)k * d.nq;
   float* dst = d.out + ((size_t)r * d.horizon + step) * d.nq;
   float run = src[0];
+  bool finite = true;
   for (int i = 0; i < d.nq; ++i) {
+    finite = finite && isfinite(src[i]);
     if (i > 0) run = run + softplus(src[i]);
     const float u = d.use_arcsinh ? sinhf(run) : run;
     dst[i] = u * sc + lc;
   }
+  if (!finite && d.nonfinite) *d.nonfinite = 1;
 }
 
 __global__ void k_gather_map(int* map, int v, int p, int ctx_p, int hp) {
@@ -417,11 +430,14 @@ void launch_window_prep(const WindowDesc& w, const PatchOut& o, hipStream_t s) {
   if (w.ps <= 0 || w.t % w.ps) throw Error(T0H_ERR_SHAPE, "prep: window not patch aligned");
   if (!o.enc_in || !o.grp || !o.att || !o.type_idx || !o.type_raw || !o.fut)
     throw Error(T0H_ERR_INVALID_ARG, "prep: null output arrays");
-  const size_t lds = prep_lds(w.t, w.ps);
-  if (lds > 160 * 1024) throw Error(T0H_ERR_UNSUPPORTED, "prep: window too long for one workgroup");
-  static std::atomic<uint64_t> lds_set{0};
-  allow_dynamic_lds(reinterpret_cast<const void*>(&k_prep_rows), lds_set);
-  hipLaunchKernelGGL(k_prep_rows, dim3(w.v), dim3(256), lds, s, w, o);
+  if (prep_fits_lds(w.t, w.ps)) {
+    static std::atomic<uint64_t> lds_set{0};
+    allow_dynamic_lds(reinterpret_cast<const void*>(&k_prep_rows<false>), lds_set);
+    hipLaunchKernelGGL(k_prep_rows<false>, dim3(w.v), dim3(256), prep_row_bytes(w.t, w.ps), s, w, o);
+  } else {
+    if (!w.rows_mem) throw Error(T0H_ERR_INVALID_ARG, "prep: long window without row memory");
+    hipLaunchKernelGGL(k_prep_rows<true>, dim3(w.v), dim3(256), 0, s, w, o);
+  }
   check_hip(hipGetLastError(), "k_prep_rows launch");
 }
 

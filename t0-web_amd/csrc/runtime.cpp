@@ -157,6 +157,12 @@ struct t0h_model {
   size_t noalloc_host_bytes = 0;
   hipEvent_t noalloc_ev = nullptr;
   bool noalloc_pending = false;
+  // Set to 1 on the device when a forecast's quantile logits are not finite (an
+  // f16 activation beyond +-65504 became inf, or the weights hold inf/NaN); lives
+  // at the end of the weights allocation.  `nonfinite_unread`: a device-output
+  // call may have set it since it was last read.
+  int* d_nonfinite = nullptr;
+  bool nonfinite_unread = false;
 };
 
 namespace t0h {
@@ -390,6 +396,8 @@ void load_model(t0h_model* m, const uint8_t* bytes, size_t len) {
     off = align256(off + pl.bytes);
     place[n] = pl;
   }
+  const size_t flag_off = off;  // the non-finite flag (256 bytes, zero)
+  off += 256;
   std::vector<uint8_t> host(off, 0);
   for (auto& kv : place) {
     const Placement& pl = kv.second;
@@ -408,8 +416,9 @@ void load_model(t0h_model* m, const uint8_t* bytes, size_t len) {
     (void)hipGetLastError();
     throw Error(T0H_ERR_OOM, "device allocation for weights failed");
   }
-  m->weights_bytes = off;
+  m->weights_bytes = flag_off;
   hip_check(hipMemcpy(m->d_weights, host.data(), off, hipMemcpyHostToDevice), "hipMemcpy weights");
+  m->d_nonfinite = reinterpret_cast<int*>(m->d_weights + flag_off);
 
   auto mat = [&](const std::string& n) {
     const Placement& pl = place.at(n);
@@ -593,6 +602,13 @@ PatchMeta patch_buffers(t0h_model* m, int v, int p) {
 // Patch encoder + transformer layers (t0-fast model.rs:727-786 ≡ t0-core model.rs:184-229).
 // Expects enc_in / patch metadata / segments and the RoPE tables of p patches
 // (ensure_rope) in the workspace.  Leaves the f32 residual stream in "x".
+// Windows of any patch count are taken (t0-core has no limit); the row count is
+// bounded so that every per-row offset of the forward fits the kernels' indexing.
+void check_window_rows(int v, int p) {
+  if ((int64_t)v * p > (int64_t)1 << 24)
+    throw Error(T0H_ERR_UNSUPPORTED, "window of " + std::to_string((int64_t)v * p) + " patch rows exceeds 16M");
+}
+
 void encode_and_layers(t0h_model* m, int v, int p, const PatchMeta& pm, float* trace_pe, float* trace_l0) {
   const t0h_config& c = m->mc.c;
   const int E = (int)c.embed_dim, ps = (int)c.patch_size, M = v * p;
@@ -677,6 +693,12 @@ void encode_and_layers(t0h_model* m, int v, int p, const PatchMeta& pm, float* t
   ad.seg_begin = seg_begin;
   ad.seg_len = seg_len;
   ad.seg_max = m->ws.seg_max;
+  if (p > T0H_LDS_PATCHES) {  // the long-window time attention's key workspace
+    const size_t P32 = (size_t)(p + 31) / 32 * 32;
+    ad.kr = ws_get<_Float16>(m, "attn_kr", (size_t)v * P32 * E);
+    ad.vt = ws_get<_Float16>(m, "attn_vt", (size_t)v * P32 * E);
+    ad.kg = ws_get<int>(m, "attn_kg", (size_t)v * P32);
+  }
   for (size_t li = 0; li < m->layers.size(); ++li) {
     const Layer& L = m->layers[li];
     if (!split || li == 0) {  // the encoder's output (F16 weights) has no split epilogue
@@ -745,9 +767,15 @@ float* decode_rows(t0h_model* m, int rows, const int* map) {
 
 // Grows every buffer encode_and_layers and decode_rows use for `rows` patch
 // rows and `dec_rows` decoded rows, so that neither allocates once launches start.
-void reserve_forward(t0h_model* m, int rows, int dec_rows) {
+void reserve_forward(t0h_model* m, int v, int p, int dec_rows) {
   const t0h_config& c = m->mc.c;
-  const size_t M = (size_t)rows, E = c.embed_dim, wide = std::max<size_t>(E, (size_t)m->enc.hid.n);
+  const size_t M = (size_t)v * p, E = c.embed_dim, wide = std::max<size_t>(E, (size_t)m->enc.hid.n);
+  if (p > T0H_LDS_PATCHES) {
+    const size_t P32 = (size_t)(p + 31) / 32 * 32;
+    ws_get<_Float16>(m, "attn_kr", (size_t)v * P32 * E);
+    ws_get<_Float16>(m, "attn_vt", (size_t)v * P32 * E);
+    ws_get<int>(m, "attn_kg", (size_t)v * P32);
+  }
   ws_get<float>(m, "x", M * E);
   ws_get<_Float16>(m, "xn", M * wide);
   ws_get<_Float16>(m, "qkv", M * 3 * E);
@@ -845,8 +873,10 @@ void forecast_window(t0h_model* m, const WindowRows& wr, float* d_out) {
     throw Error(T0H_ERR_HORIZON, "single-window forecast can't exceed max_horizon (1024) in one pass -- use forecast_rollout");
   const int t = pad_left + wr.t_ctx + padded_h;
   const int p = t / ps, ctx_p = (wr.t_ctx + pad_left) / ps, hp = padded_h / ps;
-  if (p > T0H_MAX_PATCHES)
-    throw Error(T0H_ERR_UNSUPPORTED, "window of " + std::to_string(p) + " patches exceeds " + std::to_string(T0H_MAX_PATCHES));
+  if (m->ws.arena.on && p > T0H_NOALLOC_MAX_PATCHES)
+    throw Error(T0H_ERR_UNSUPPORTED, "no-allocation forecast: window of " + std::to_string(p) + " patches exceeds " +
+                                         std::to_string(T0H_NOALLOC_MAX_PATCHES));
+  check_window_rows(v, p);
   hipStream_t s = m->stream;
 
   // dense group ids for the device
@@ -861,11 +891,12 @@ void forecast_window(t0h_model* m, const WindowRows& wr, float* d_out) {
   }
   // every device buffer of the window is sized before the first upload or launch
   const PatchMeta pm = patch_buffers(m, v, p);
-  reserve_forward(m, v * p, v * std::max(hp, 1));
+  reserve_forward(m, v, p, v * std::max(hp, 1));
   int* map = ws_get<int>(m, "dec_map", (size_t)v * std::max(hp, 1));
   ws_get<int64_t>(m, "win_off", v);
   for (const char* n : {"win_len", "win_grp", "perm", "seg_begin", "seg_len"}) ws_get<int>(m, n, v);
   ws_get<float>(m, "rope", m->layers.size() * 2 * (size_t)p * 128);
+  uint8_t* prep_rows = prep_fits_lds(t, ps) ? nullptr : ws_get<uint8_t>(m, "prep_rows", (size_t)v * prep_row_bytes(t, ps));
 
   const int64_t* d_off = put_cached(m, "win_off", wr.src_off.data(), v);
   const int* d_len = put_cached(m, "win_len", wr.len.data(), v);
@@ -887,6 +918,7 @@ void forecast_window(t0h_model* m, const WindowRows& wr, float* d_out) {
   w.use_arcsinh = c.scaler_use_arcsinh;
   w.variance_offset = c.scaler_variance_offset;
   w.eps = c.scaler_eps;
+  w.rows_mem = prep_rows;
 
   auto launches = [&]() {
     {
@@ -904,6 +936,7 @@ void forecast_window(t0h_model* m, const WindowRows& wr, float* d_out) {
     od.patch_loc = pm.patch_loc;
     od.patch_scale = pm.patch_scale;
     od.out = d_out;
+    od.nonfinite = m->d_nonfinite;
     od.v = v;
     od.p = p;
     od.ctx_p = ctx_p;
@@ -936,6 +969,30 @@ float* upload_contexts(t0h_model* m, const float* ctx, size_t n) { return put(m,
 void check_out(size_t out_len, size_t want) {
   if (out_len != want)
     throw Error(T0H_ERR_INVALID_ARG, "output buffer holds " + std::to_string(out_len) + " floats, expected " + std::to_string(want));
+}
+
+// The non-finite flag around a host-output call: cleared first if a device-output
+// call may have set it, read back with the results (the caller synchronizes after).
+void numerics_begin(t0h_model* m) {
+  if (!m->nonfinite_unread) return;
+  hip_check(hipMemsetAsync(m->d_nonfinite, 0, sizeof(int), m->stream), "hipMemsetAsync");
+  m->nonfinite_unread = false;
+}
+void numerics_read(t0h_model* m, int* host_flag) { download(m, host_flag, m->d_nonfinite, 1); }
+void numerics_end(t0h_model* m, int host_flag);
+// Waits for a host-output call's results and raises T0H_ERR_NUMERIC if they are not finite.
+void finish_host_call(t0h_model* m) {
+  int nf = 0;
+  numerics_read(m, &nf);
+  sync(m);
+  numerics_end(m, nf);
+}
+void numerics_end(t0h_model* m, int host_flag) {
+  if (!host_flag) return;
+  hip_check(hipMemsetAsync(m->d_nonfinite, 0, sizeof(int), m->stream), "hipMemsetAsync");
+  sync(m);
+  throw Error(T0H_ERR_NUMERIC,
+              "forecast produced non-finite model outputs: an f16 activation exceeded 65504, or the weights are not finite");
 }
 
 // forecast_rollout helpers (quantile.rs:16-76)
@@ -1011,6 +1068,7 @@ int median_index(const t0h_config& c) {
 // Exposed for the rollout driver.
 void forecast_host(t0h_model* m, const float* ctx, size_t v, size_t t_ctx, size_t horizon, float* out) {
   const int nq = (int)m->mc.c.n_quantiles;
+  numerics_begin(m);
   float* d_ctx = upload_contexts(m, ctx, v * t_ctx);
   WindowRows wr;
   wr.t_ctx = (int)t_ctx;
@@ -1024,13 +1082,14 @@ void forecast_host(t0h_model* m, const float* ctx, size_t v, size_t t_ctx, size_
   float* d_out = ws_get<float>(m, "out", std::max<size_t>(1, v * horizon * nq));
   forecast_window(m, wr, d_out);
   download(m, out, d_out, v * horizon * nq);
-  sync(m);
+  finish_host_call(m);
 }
 
 void forecast_batch_host(t0h_model* m, const float* ctx, size_t n, size_t t_ctx, size_t horizon, size_t chunk,
                          float* out) {
   const int nq = (int)m->mc.c.n_quantiles;
   chunk = (chunk == 0 || chunk > n) ? n : chunk;
+  numerics_begin(m);
   float* d_ctx = upload_contexts(m, ctx, n * t_ctx);
   float* d_out = ws_get<float>(m, "out", std::max<size_t>(1, n * horizon * nq));
   for (size_t start = 0; start < n; start += chunk) {
@@ -1047,7 +1106,7 @@ void forecast_batch_host(t0h_model* m, const float* ctx, size_t n, size_t t_ctx,
     forecast_window(m, wr, d_out + start * horizon * nq);
   }
   download(m, out, d_out, n * horizon * nq);
-  sync(m);
+  finish_host_call(m);
 }
 
 }  // namespace t0h
@@ -1127,7 +1186,7 @@ int t0h_model_load_gguf(t0h_ctx* ctx, const uint8_t* bytes, size_t len, t0h_mode
     // pinned staging for the no-allocation entry point: RoPE tables of the longest
     // window plus per-row metadata for as many rows as the scratch can hold
     const size_t rows_max = T0H_NOALLOC_SCRATCH_BYTES / (4 * (size_t)m->mc.c.embed_dim);
-    m->noalloc_host_bytes = m->layers.size() * 2 * (size_t)T0H_MAX_PATCHES * 128 * 4 + 32 * rows_max + 4096;
+    m->noalloc_host_bytes = m->layers.size() * 2 * (size_t)T0H_NOALLOC_MAX_PATCHES * 128 * 4 + 32 * rows_max + 4096;
     if (hipHostMalloc(&m->noalloc_host, m->noalloc_host_bytes, hipHostMallocDefault) != hipSuccess) {
       (void)hipGetLastError();
       m->noalloc_host = nullptr;
@@ -1264,7 +1323,7 @@ int t0h_forward(t0h_model* m, const t0h_series* sr, float* out, size_t out_len, 
   const int v = (int)sr->v, t = (int)sr->t, p = t / ps;
   check_out(out_len, (size_t)v * p * ps * nq);
   if (v == 0 || p == 0) return T0H_OK;
-  if (p > T0H_MAX_PATCHES) throw Error(T0H_ERR_UNSUPPORTED, "series exceeds the maximum patch count");
+  check_window_rows(v, p);
   const size_t n = (size_t)v * t;
   for (size_t i = 0; i < n; ++i)
     if (sr->variate_type[i] >= m->n_types) throw Error(T0H_ERR_INVALID_ARG, "variate type out of range of the type embeddings");
@@ -1348,6 +1407,7 @@ int t0h_forecast_batch_rows_chunked(t0h_model* m, const float* contexts, const s
   }
   require(contexts || total == 0, "t0h_forecast_batch_rows_chunked: contexts is NULL");
   chunk = (chunk == 0 || chunk > n) ? n : chunk;
+  numerics_begin(m);
   float* d_ctx = upload_contexts(m, contexts, total);
   float* d_out = ws_get<float>(m, "out", std::max<size_t>(1, n * horizon * nq));
   for (size_t start = 0; start < n; start += chunk) {  // lib.rs:200-240
@@ -1366,7 +1426,7 @@ int t0h_forecast_batch_rows_chunked(t0h_model* m, const float* contexts, const s
     forecast_window(m, wr, d_out + start * horizon * nq);
   }
   download(m, out, d_out, n * horizon * nq);
-  sync(m);
+  finish_host_call(m);
   API_END
 }
 
@@ -1390,12 +1450,13 @@ int t0h_forecast_grouped(t0h_model* m, const float* contexts, const int64_t* row
   WindowRows wr;
   wr.t_ctx = (int)t_ctx;
   wr.horizon = (int)horizon;
+  numerics_begin(m);
   wr.d_ctx = upload_contexts(m, contexts, n_rows * t_ctx);
   grouped_rows(wr, row_group, n_rows, t_ctx);
   float* d_out = ws_get<float>(m, "out", std::max<size_t>(1, n_rows * horizon * nq));
   forecast_window(m, wr, d_out);
   download(m, out, d_out, n_rows * horizon * nq);
-  sync(m);
+  finish_host_call(m);
   API_END
 }
 
@@ -1410,6 +1471,7 @@ int t0h_forecast_grouped_dev(t0h_model* m, const float* d_contexts, const int64_
   wr.horizon = (int)horizon;
   wr.d_ctx = d_contexts;
   grouped_rows(wr, row_group, n_rows, t_ctx);
+  m->nonfinite_unread = true;
   forecast_window(m, wr, d_out);
   API_END
 }
@@ -1448,7 +1510,20 @@ int t0h_forecast_grouped_dev_noalloc(t0h_model* m, const float* d_contexts, cons
       x.named.clear();
     }
   } off{m};
+  m->nonfinite_unread = true;
   forecast_window(m, wr, d_out);
+  API_END
+}
+
+int t0h_model_check_numerics(t0h_model* m) {
+  API_BEGIN
+  require(m, "t0h_model_check_numerics: NULL model");
+  bind_device(m);
+  int nf = 0;
+  numerics_read(m, &nf);
+  sync(m);
+  m->nonfinite_unread = false;
+  numerics_end(m, nf);
   API_END
 }
 
@@ -1462,6 +1537,7 @@ int t0h_forecast_grouped_ar(t0h_model* m, const float* contexts, const int64_t* 
   check_out(out_len, n_rows * steps * horizon * nq);
   if (steps == 0) return T0H_OK;
   const int qi = median_index(m->mc.c);
+  numerics_begin(m);
   float* ctx_a = put(m, "ar_ctx_a", contexts, n_rows * t_ctx);
   float* ctx_b = ws_get<float>(m, "ar_ctx_b", n_rows * t_ctx);
   float* step_out = ws_get<float>(m, "ar_step", n_rows * horizon * nq);
@@ -1478,7 +1554,7 @@ int t0h_forecast_grouped_ar(t0h_model* m, const float* contexts, const int64_t* 
     std::swap(ctx_a, ctx_b);
   }
   download(m, out, result, n_rows * steps * horizon * nq);
-  sync(m);
+  finish_host_call(m);
   API_END
 }
 

@@ -22,7 +22,7 @@ LIB_PATH = os.path.join(_HERE, "libt0hip.so")
 F32, F16, Q4_0, Q8_0 = 0, 1, 2, 8
 MAX_Q = 64
 MAX_HORIZON = 1024
-MAX_PATCHES = 256
+NOALLOC_MAX_PATCHES = 256
 MASK_VALID, MASK_PAD, MASK_MISSING, MASK_CENSORED, MASK_WITHHELD = 0, 1, 2, 3, 4
 VT_TARGET, VT_HISTORICAL, VT_FUTURE = 0, 1, 2
 
@@ -30,7 +30,7 @@ STATUS = {
     0: "OK", -1: "INVALID_ARG", -2: "GGUF_MAGIC", -3: "GGUF_VERSION", -4: "GGUF_TENSOR_TYPE",
     -5: "GGUF_META_TYPE", -6: "GGUF_BOUNDS", -7: "MISSING_TENSOR", -8: "METADATA", -9: "HORIZON",
     -10: "FUTURE_ROWS", -11: "NO_DEVICE", -12: "HIP", -13: "SHAPE", -14: "UNSUPPORTED", -15: "OOM",
-    -16: "SAFETENSORS", -17: "CONFIG",
+    -16: "SAFETENSORS", -17: "CONFIG", -18: "NUMERIC",
 }
 
 
@@ -74,7 +74,7 @@ _lib = None
 SYMBOLS = [
     "t0h_last_error", "t0h_abi_version", "t0h_ctx_create", "t0h_ctx_destroy", "t0h_gguf_inspect",
     "t0h_model_load_gguf", "t0h_model_destroy", "t0h_model_config", "t0h_model_weight_bytes", "t0h_model_stream",
-    "t0h_model_workspace", "t0h_model_profile", "t0h_model_profile_kind", "t0h_model_profile_entry", "t0h_model_graph_replay", "t0h_forward", "t0h_forecast", "t0h_forecast_batch_chunked",
+    "t0h_model_workspace", "t0h_model_profile", "t0h_model_profile_kind", "t0h_model_profile_entry", "t0h_model_graph_replay", "t0h_model_check_numerics", "t0h_forward", "t0h_forecast", "t0h_forecast_batch_chunked",
     "t0h_forecast_batch_rows_chunked", "t0h_forecast_grouped", "t0h_forecast_grouped_dev",
     "t0h_forecast_grouped_dev_noalloc",
     "t0h_forecast_grouped_ar", "t0h_forecast_rollout", "t0h_dequant", "t0h_gemm_q", "t0h_gemm_f16", "t0h_row_bytes",
@@ -111,6 +111,7 @@ def lib():
     L.t0h_model_profile_kind.argtypes = [P, C.c_char_p]
     L.t0h_model_profile_entry.argtypes = [P, S, C.c_char_p, S, C.POINTER(C.c_uint64), C.POINTER(C.c_double)]
     L.t0h_model_graph_replay.argtypes = [P, I]
+    L.t0h_model_check_numerics.argtypes = [P]
     L.t0h_forward.argtypes = [P, C.POINTER(Series), P, S, P, P]
     L.t0h_forecast.argtypes = [P, P, S, S, S, P, S]
     L.t0h_forecast_batch_chunked.argtypes = [P, P, S, S, S, S, P, S]
@@ -310,6 +311,11 @@ class GpuModel:
     def graph_replay(self, enable=True):
         """Capture and replay each window forward as a HIP graph (default) or run it eagerly."""
         _check(lib().t0h_model_graph_replay(self.h, int(enable)))
+
+    def check_numerics(self):
+        """Wait for the model's stream; raise T0HipError("NUMERIC") if a forecast since the last
+        check (device-output calls included) produced non-finite model outputs."""
+        _check(lib().t0h_model_check_numerics(self.h))
 
     def workspace(self):
         r, a = C.c_uint64(), C.c_uint64()

@@ -147,6 +147,34 @@ def test_forward_future_pad_and_groups(models, t0hip, oracle, rng, q, inconsiste
 
 
 @pytest.mark.parametrize("q", [8, 2])
+def test_forward_long_window(models, t0hip, oracle, rng, q):
+    """A window longer than the LDS-resident time attention holds (300 patches > 256): the keys
+    stream through workspace with an online softmax, on the same mask branches as above (FUTURE,
+    whole-PAD, negative-group and inconsistent-group rows)."""
+    gm, om = models[("small", q)]
+    sc, mask, grp, vt = mixed_series(rng, t=300 * 32, inconsistent=True)
+    out, pe, l0 = t0hip.forward(gm, sc, mask, grp, vt, trace=True)
+    want, wpe, wl0 = om.forward(sc, mask, grp, vt, trace=True)
+    assert_close(pe, wpe, tol=2e-3)
+    assert_close(l0, wl0, tol=5e-3)
+    assert_close(out, want)
+
+
+@pytest.mark.parametrize("t_ctx,h", [(9000, 64), (20000, 40)])
+def test_forecast_long_context(models, t0hip, oracle, engine, rng, t_ctx, h):
+    """Contexts past 256 patches (t0-core takes any length): 9000 steps (284 patches, the streamed
+    time attention) and 20000 steps (628 patches, where the window prep's per-row arrays no longer
+    fit the LDS and live in device memory), two series with NaN gaps."""
+    gm, om = models[("small", 8)]
+    ctx = nan_gaps(rng, sine_mix(rng, 2, t_ctx), frac=0.1, lo=16, hi=128)
+    got = t0hip.forecast(engine, gm, ctx, 2, t_ctx, h)
+    want = om.forecast(ctx, 2, t_ctx, h)
+    scale = row_scale(ctx)
+    report(f"long context {t_ctx}", got, want, scale)
+    assert_close(got, want, scale=scale)
+
+
+@pytest.mark.parametrize("q", [8, 2])
 def test_forecast_reference_fixture_inputs(models, t0hip, oracle, engine, q):
     """t0-cli parity --backend fast pattern (main.rs:583-664): same GGUF, same fixture contexts,
     GPU forecast vs the CPU path, context 512 / horizon 96."""
@@ -353,11 +381,51 @@ def test_error_paths_on_device(models, t0hip, engine, rng):
         t0hip.forecast(engine, gm, ctx, 1, 64, 1025)
     assert e.value.status == "HORIZON"
     with pytest.raises(t0hip.T0HipError) as e:
-        t0hip.forecast(engine, gm, sine_mix(rng, 1, 9000), 1, 9000, 32)
-    assert e.value.status == "UNSUPPORTED"
-    with pytest.raises(t0hip.T0HipError) as e:
         t0hip.forecast_grouped(engine, gm, ctx, np.array([-1]), 64, 32)
     assert e.value.status == "INVALID_ARG"
+
+
+def test_numeric_guard_on_f16_overflow(t0hip, oracle, engine, torch_cuda, rng):
+    """An f16 activation beyond 65504 (the SwiGLU hidden of layer 0, its gate/up weights scaled by
+    2000) becomes inf on the GPU where the reference's f32 path stays finite: the host-output entry
+    points return NUMERIC, a device-output call leaves the report to check_numerics, which clears
+    it; a model without the overflow is unaffected."""
+    import json
+
+    import safetensors.numpy
+    from test_oracle import _tensor_names
+    g = t0hip.synth_model_gguf(t0hip.make_config(**TINY), quant=0, seed=17)
+    om = oracle.Model(g)
+    tensors = {n: np.ascontiguousarray(om.tensor(n), np.float32) for n in _tensor_names(g)}
+    tensors["transformer.layers.0.mlp.0.weight"] *= np.float32(2000.0)
+    config = {k: TINY[k] for k in ("embed_dim", "num_layers", "num_heads", "mlp_hidden_dim", "patch_size",
+                                   "group_every_n")}
+    config.update(dropout=0.0, quantile_levels=[float(np.float32(q)) for q in TINY["quantile_levels"]])
+    big = t0hip.export_gguf_from_safetensors(safetensors.numpy.save(tensors), json.dumps(config), 0)
+    gm = t0hip.load_model_from_gguf(engine, big)
+    ctx = sine_mix(rng, 2, 256)
+    want = oracle.Model(big).forecast(ctx, 2, 256, 32)
+    assert np.isfinite(want).all()
+    for call in (lambda: t0hip.forecast(engine, gm, ctx, 2, 256, 32),
+                 lambda: t0hip.forecast_grouped(engine, gm, ctx, np.array([0, 1]), 256, 32),
+                 lambda: t0hip.forecast_grouped_ar(engine, gm, ctx, np.array([0, 1]), 256, 32, 2)):
+        with pytest.raises(t0hip.T0HipError) as e:
+            call()
+        assert e.value.status == "NUMERIC", e.value
+    torch = torch_cuda
+    d_x = torch.tensor(ctx, dtype=torch.float32, device="cuda")
+    out = torch.empty((2, 32, 5), dtype=torch.float32, device="cuda")
+    torch.cuda.synchronize()
+    t0hip.forecast_grouped_dev(gm, d_x.data_ptr(), np.array([0, 1]), 256, 32, out.data_ptr())
+    with pytest.raises(t0hip.T0HipError) as e:
+        gm.check_numerics()
+    assert e.value.status == "NUMERIC"
+    gm.check_numerics()  # read and cleared
+    ok = t0hip.load_model_from_gguf(engine, g)
+    got = t0hip.forecast(engine, ok, ctx, 2, 256, 32)
+    assert_close(got, om.forecast(ctx, 2, 256, 32), scale=row_scale(ctx))
+    t0hip.forecast_grouped_dev(ok, d_x.data_ptr(), np.array([0, 1]), 256, 32, out.data_ptr())
+    ok.check_numerics()
 
 
 def test_profiler_all_kinds_and_one_kind(models, t0hip, engine, rng):
@@ -401,6 +469,20 @@ def test_baseline_model_forecast(t0hip, oracle, engine, rng):
     want = om.forecast(ctx, 1, 2048, 64)
     assert_close(got, want, scale=row_scale(ctx))
     assert_close(got, want)
+
+
+def test_baseline_model_long_context(t0hip, oracle, engine, rng):
+    """The BASELINE model on one series of 12,000 steps (377 patches): the streamed time attention
+    at full width (12 heads of 64).  Gated in the series' own scale (about 2 here); the raw figure
+    is printed (5.4e-3 measured: about twice the normalized one, as the scale says)."""
+    g = t0hip.synth_model_gguf(t0hip.make_config(**BASELINE), quant=8, seed=0)
+    gm = t0hip.load_model_from_gguf(engine, g)
+    om = oracle.Model(g)
+    ctx = sine_mix(rng, 1, 12000)
+    got = t0hip.forecast(engine, gm, ctx, 1, 12000, 64)
+    want = om.forecast(ctx, 1, 12000, 64)
+    report("baseline long context", got, want, row_scale(ctx))
+    assert_close(got, want, scale=row_scale(ctx))
 
 
 def test_config5_windows_small_model(t0hip, oracle, engine, rng):

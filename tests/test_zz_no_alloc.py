@@ -49,6 +49,14 @@ def test_noalloc_matches_allocating_entry_point(t0hip, engine, torch_cuda, rng):
     assert e.value.status == "UNSUPPORTED" and "scratch" in str(e.value)
     torch.cuda.synchronize()
     assert bool((out == 7.0).all())
+    # a window past the no-allocation limit (300 patches > NOALLOC_MAX_PATCHES) is rejected too
+    d_long = torch.zeros((1, 300 * 32 - 64), dtype=torch.float32, device="cuda")
+    torch.cuda.synchronize()
+    with pytest.raises(t0hip.T0HipError) as e:
+        t0hip.forecast_grouped_dev_noalloc(gm, d_long.data_ptr(), np.array([0]), 300 * 32 - 64, 64, out.data_ptr())
+    assert e.value.status == "UNSUPPORTED" and "patches" in str(e.value)
+    torch.cuda.synchronize()
+    assert bool((out == 7.0).all())
     # still usable after the rejection
     d_x, groups, t_ctx, h = inputs[1]
     again = torch.empty((groups.size, h, 9), dtype=torch.float32, device="cuda")
