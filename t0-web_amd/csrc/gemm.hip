@@ -1452,6 +1452,8 @@ __global__ __launch_bounds__(256) void k_gemv(const GemmDesc d) {
 // trick, the offset removed and d applied in packed f16 (one rounding of d*q).
 template <int WT>
 __device__ __forceinline__ half8 dq_frag(const uint32_t* r, int c, int h) {
+  if constexpr (WT == T0H_F16)  // the lane's 32 weights of the step as they are: slice c is dwords 4c..4c+3
+    return __builtin_bit_cast(half8, make_uint4(r[4 * c], r[4 * c + 1], r[4 * c + 2], r[4 * c + 3]));
   const uint32_t qsel = h ? 0x07060504u : 0x05040302u;
   const uint32_t dsel = h ? 0x03020302u : 0x01000100u;
   const int i = WT == T0H_Q8_0 ? 2 * c : 2 * (c & 1);
@@ -1480,14 +1482,17 @@ __device__ __forceinline__ half8 dq_frag(const uint32_t* r, int c, int h) {
 
 template <int WT, bool A32, int EPI, int TI, int KR, int TJ, int RN>
 __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2))) void k_gemm_mid(const GemmDesc d) {
-  constexpr bool SWI = EPI == EPI_SWIGLU_F16;
-  constexpr int NWD = WT == T0H_Q8_0 ? 9 : 5, SWD = WT == T0H_Q8_0 ? 17 : 9;
+  constexpr bool SWI = EPI == EPI_SWIGLU_F16, F16W = WT == T0H_F16;
+  // dwords of a step a lane loads / of a weight row per step (F16: the lane's 32
+  // contiguous values; K % 32 == 0, so a lane half of the last step may be past K)
+  constexpr int NWD = F16W ? 16 : WT == T0H_Q8_0 ? 9 : 5, SWD = F16W ? 32 : WT == T0H_Q8_0 ? 17 : 9;
   static_assert(!SWI || TJ == 1, "SwiGLU tiles pair gate and up columns in one 32-column group");
   constexpr int W = SWI ? 16 : 32 * TJ;  // output columns per tile
   extern __shared__ __align__(16) float red[];
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6, nw = blockDim.x >> 6;
   const int h = lane >> 5, lc = lane & 31;
-  const int M = d.M, N = d.N, K = d.K, KT = K / 64;
+  const int M = d.M, N = d.N, K = d.K, KT = (K + 63) / 64;
+  auto half_ok = [&](int step) { return !F16W || step * 64 + 32 * h < K; };
   const int strips = (N + W - 1) / W;
   const int tn = blockIdx.x % strips, m0 = (blockIdx.x / strips) * (32 * TI);
   // split RMSNorm consumer: row scales after the partial tiles and the staging
@@ -1510,14 +1515,24 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2))) void k
       wrow = (tn * TJ + j) * 32 + lc;
       ok = wrow < N;
     }
-    const uint32_t* wsrc =
-        static_cast<const uint32_t*>(d.w) + (size_t)(ok ? wrow : 0) * ((K / 32) * block_bytes(WT) / 4) + h * (NWD - 1);
+    const uint32_t* wsrc = static_cast<const uint32_t*>(d.w) +
+                           (size_t)(ok ? wrow : 0) * (F16W ? K / 2 : (K / 32) * block_bytes(WT) / 4) +
+                           h * (F16W ? NWD : NWD - 1);
 #pragma unroll
     for (int s = 0; s < KR; ++s)
       if (s0 + s < KT) {
         const uint32_t* src = wsrc + (s0 + s) * SWD;  // NWD contiguous dwords
+        if constexpr (F16W) {
+          const bool in = half_ok(s0 + s);
 #pragma unroll
-        for (int i = 0; i < NWD; ++i) wr[j][s][i] = src[i];
+          for (int q = 0; q < 4; ++q) {
+            const uint4 u = in ? reinterpret_cast<const uint4*>(src)[q] : make_uint4(0, 0, 0, 0);
+            wr[j][s][4 * q] = u.x, wr[j][s][4 * q + 1] = u.y, wr[j][s][4 * q + 2] = u.z, wr[j][s][4 * q + 3] = u.w;
+          }
+        } else {
+#pragma unroll
+          for (int i = 0; i < NWD; ++i) wr[j][s][i] = src[i];
+        }
       }
   }
   half8 af[KR][4][TI];
@@ -1530,7 +1545,9 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2))) void k
 #pragma unroll
         for (int c = 0; c < 4; ++c) {
           const size_t k = (size_t)(s0 + s) * 64 + 32 * h + 8 * c;
-          if (A32) {
+          if (!half_ok(s0 + s)) {
+            af[s][c][i] = (half8){};
+          } else if (A32) {
             const float4* src = reinterpret_cast<const float4*>(static_cast<const float*>(d.a) + row + k);
             const float4 x0 = src[0], x1 = src[1];
             af[s][c][i] = (half8){(_Float16)x0.x, (_Float16)x0.y, (_Float16)x0.z, (_Float16)x0.w,
@@ -2106,13 +2123,16 @@ int device_cus() {
 // 256 rows (and not SwiGLU) a workgroup may cover four or two 32-column groups
 // (two past K = 1024), so the activation block is read by a quarter or half as
 // many workgroups, when that still fills about one round of the CUs.
-bool mid_ok(const GemmDesc& d) { return d.K % 64 == 0 && d.K <= (d.a_f32 ? 2048 : 4096); }
+bool mid_ok(const GemmDesc& d) {
+  if (d.wtype == T0H_F16) return d.K % 32 == 0 && d.K <= 2048;  // (16-dword spans: at most 4 steps a wave)
+  return d.K % 64 == 0 && d.K <= (d.a_f32 ? 2048 : 4096);
+}
 
 // Workgroups of a TJ-group launch with 32-row tiles, and whether they fill
 // between three quarters of a round and one round of the device's CUs (the
 // LDS of the partial tiles bounds the workgroups per CU).
 bool mid_groups_fit(const GemmDesc& d, int tj, int kr) {
-  const int KT = d.K / 64, nw = std::max(1, (KT + kr - 1) / kr), cus = device_cus();
+  const int KT = (d.K + 63) / 64, nw = std::max(1, (KT + kr - 1) / kr), cus = device_cus();
   const long long wgs = (long long)((d.N + 32 * tj - 1) / (32 * tj)) * ((d.M + 31) / 32);
   const size_t lds = (size_t)nw * tj * 16 * 64 * 4 + (size_t)32 * (32 * tj + 4) * 4;
   const long long per_cu = std::max<long long>(1, (long long)(160 * 1024 / lds));
@@ -2121,8 +2141,8 @@ bool mid_groups_fit(const GemmDesc& d, int tj, int kr) {
 
 template <int WT, bool A32, int EPI>
 void dispatch_mid(const GemmDesc& d, hipStream_t s) {
-  const int KT = d.K / 64;
-  if constexpr (EPI != EPI_SWIGLU_F16) {
+  const int KT = (d.K + 63) / 64;
+  if constexpr (EPI != EPI_SWIGLU_F16 && WT != T0H_F16) {  // (F16 spans are 16 dwords: one column group)
     if (d.M >= 256 && KT <= 32) {
       const int kr = KT <= 16 ? 2 : 4;
       if (kr == 2 && mid_groups_fit(d, 4, 2)) return run_gemm_mid<WT, A32, EPI, 1, 2, 4>(d, s);
@@ -2135,24 +2155,23 @@ void dispatch_mid(const GemmDesc& d, hipStream_t s) {
   // 32-row tiles below 256 rows: more workgroups, each with a shorter operand
   // set (measured at M = 66 / 198, Q8_0: w2 14.0 -> 9.9 / 14.2 -> 10.2 us, QKV
   // 6.9 -> 5.9, wO 6.8 -> 5.9, SwiGLU 7.2 -> 6.8 / 11.6 -> 10.7 us)
-  if (A32 || d.M < 256 || KT > 32) {
+  // (F16 spans hold twice the registers: 64-row tiles only with two steps a wave)
+  if (A32 || d.M < 256 || KT > 32 || (WT == T0H_F16 && KT > 16)) {
     if (KT <= 16) return run_gemm_mid<WT, A32, EPI, 1, 2>(d, s);
     if (KT <= 32) return run_gemm_mid<WT, A32, EPI, 1, 4>(d, s);
-    if constexpr (!A32) return run_gemm_mid<WT, A32, EPI, 1, 8>(d, s);
+    if constexpr (!A32 && WT != T0H_F16) return run_gemm_mid<WT, A32, EPI, 1, 8>(d, s);
   } else {
     if (KT <= 16) return run_gemm_mid<WT, A32, EPI, 2, 2>(d, s);
-    return run_gemm_mid<WT, A32, EPI, 2, 4>(d, s);
+    if constexpr (WT != T0H_F16) return run_gemm_mid<WT, A32, EPI, 2, 4>(d, s);
   }
   throw Error(T0H_ERR_UNSUPPORTED, "gemm: shape outside the medium-M kernel");
 }
 
 template <int WT, bool A32, int EPI>
 void dispatch_w(const GemmDesc& d, int force, hipStream_t s) {
-  if constexpr (WT != T0H_F16) {
-    // medium M (force 0) or force 9
-    const bool mid = force == 0 && d.M > 16 && d.M < MID_M_MAX && (long long)d.M * d.N <= MID_MN_MAX;
-    if ((force == FORCE_MID || mid) && mid_ok(d)) return dispatch_mid<WT, A32, EPI>(d, s);
-  }
+  // medium M (force 0) or FORCE_MID
+  const bool mid = force == 0 && d.M > 16 && d.M < MID_M_MAX && (long long)d.M * d.N <= MID_MN_MAX;
+  if ((force == FORCE_MID || mid) && mid_ok(d)) return dispatch_mid<WT, A32, EPI>(d, s);
   const bool mfma = force == 1 || (force >= 3 && force != FORCE_MID) || (force == 0 && d.M > 16);
   if (mfma) {
     const int tile = force >= 3 ? force - 2 : 0;
@@ -2178,12 +2197,11 @@ void dispatch_type(const GemmDesc& d, int force, hipStream_t s) {
 }  // namespace
 
 // Mirrors the automatic choice (force 0) of dispatch_w: only the medium-M kernel
-// (quantized weights, f16 activations, K % 64 == 0, 16 < M < 1024 up to
-// MID_MN_MAX outputs) has the split RMSNorm epilogues.
+// (f16 activations, 16 < M < 1024 up to MID_MN_MAX outputs, the K of mid_ok) has
+// the split RMSNorm epilogues.
 namespace {
 bool mid_auto(const GemmDesc& d) {
-  return d.wtype != T0H_F16 && !d.a_f32 && d.M > 16 && d.M < MID_M_MAX && (long long)d.M * d.N <= MID_MN_MAX &&
-         mid_ok(d);
+  return !d.a_f32 && d.M > 16 && d.M < MID_M_MAX && (long long)d.M * d.N <= MID_MN_MAX && mid_ok(d);
 }
 }  // namespace
 bool rownorm_producer_ok(const GemmDesc& d) {

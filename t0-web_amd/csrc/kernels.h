@@ -67,19 +67,25 @@ bool rownorm_consumer_ok(const GemmDesc& d);
 
 void launch_gemm(const GemmDesc& d, hipStream_t s);
 // force = 0: pick by shape (M <= 16 small-M kernels; 16 < M < 1024 the split-K
-// medium-M kernel up to 512 x 2304 outputs; else MFMA tiles); 1: MFMA tile kernel (tile
+// medium-M kernel up to 512 x 2304 outputs (F16 weights too); else MFMA tiles); 1: MFMA tile kernel (tile
 // by shape); 2: small-M kernels; 3 / 4 / 5: MFMA kernel with 128x128 / 256x128 / 256x256
 // tiles; 6: 256x256 DMA-fed kernel; 7 / 8: 256x256 / 256x128 kernels with
 // register-dequantized weight fragments, 9 / 10: the 256x128 one with 192 / 128 rows (6-10:
-// K % 64 == 0, f16 activations, quantized weights); FORCE_MID: medium-M kernel (K % 64 == 0,
-// quantized weights).
+// K % 64 == 0, f16 activations, quantized weights); FORCE_MID: medium-M kernel (quantized
+// weights with K % 64 == 0, or F16 weights with K % 32 == 0 and K <= 2048).
 constexpr int FORCE_MID = 32;
 void launch_gemm_forced(const GemmDesc& d, int force, hipStream_t s);
 void launch_dequant(int type, const void* w, size_t n, float* out, hipStream_t s);
 
 // ---- norms -----------------------------------------------------------------
-// out_f16[r] = x[map ? map[r] : r] / sqrt(mean(x^2) + 1e-8) * scale
-void launch_rmsnorm(const float* x, const float* scale, _Float16* out, const int* row_map, int rows, int dim,
+// out_f16[t] = x[gth.row(t)] / sqrt(mean(x^2) + 1e-8) * scale
+// Rows a launch reads: row t itself, or (hp > 0, the forecast rows of a window)
+// row (t / hp) * p + ctx_p - 1 + t % hp, patch ctx_p - 1 + h of window row t / hp.
+struct RowGather {
+  int p = 0, ctx_p = 0, hp = 0;
+  __host__ __device__ int row(int t) const { return hp ? (t / hp) * p + ctx_p - 1 + t % hp : t; }
+};
+void launch_rmsnorm(const float* x, const float* scale, _Float16* out, const RowGather& gth, int rows, int dim,
                     hipStream_t s);
 
 // ---- attention ---------------------------------------------------------------
@@ -173,8 +179,6 @@ struct ForecastOutDesc {
   int v = 0, p = 0, ctx_p = 0, hp = 0, ps = 0, nq = 0, horizon = 0, use_arcsinh = 1;
 };
 void launch_forecast_out(const ForecastOutDesc& d, hipStream_t s);
-// Decoder row gather map: map[r*hp + h] = r*p + ctx_p - 1 + h
-void launch_gather_map(int* map, int v, int p, int ctx_p, int hp, hipStream_t s);
 // AR window update: ctx[r, :] <- (ctx[r, horizon:] ++ out[r, :, q_idx]) trailing t_ctx values.
 void launch_ar_shift(float* ctx_next, const float* ctx, const float* out, int v, int t_ctx, int horizon, int nq,
                      int q_idx, hipStream_t s);

@@ -20,12 +20,12 @@ void check_hip(hipError_t e, const char* what) {
 }
 
 // ---- RMSNorm (ops.rs:12-17; rmsnorm_full.wgsl): one wave per row ------------------
-__global__ __launch_bounds__(256) void k_rmsnorm(const float* x, const float* scale, _Float16* out, const int* map,
+__global__ __launch_bounds__(256) void k_rmsnorm(const float* x, const float* scale, _Float16* out, const RowGather gth,
                                                  int rows, int dim) {
   const int lane = threadIdx.x & 63;
   const int row = blockIdx.x * 4 + (threadIdx.x >> 6);
   if (row >= rows) return;
-  const float* src = x + (size_t)(map ? map[row] : row) * dim;
+  const float* src = x + (size_t)gth.row(row) * dim;
   float ss = 0.0f;
   for (int c = lane * 4; c < dim; c += 256) {
     const float4 v = *reinterpret_cast<const float4*>(src + c);
@@ -48,11 +48,11 @@ __global__ __launch_bounds__(256) void k_rmsnorm(const float* x, const float* sc
 // memory round trip), sums over DPP lane moves and row swaps, normalizes from
 // registers.
 __global__ __launch_bounds__(256) void k_rmsnorm_reg(const float* x, const float* scale, _Float16* out,
-                                                     const int* map, int rows, int dim) {
+                                                     const RowGather gth, int rows, int dim) {
   const int lane = threadIdx.x & 63;
   const int row = blockIdx.x * 4 + (threadIdx.x >> 6);
   if (row >= rows) return;
-  const float* src = x + (size_t)(map ? map[row] : row) * dim;
+  const float* src = x + (size_t)gth.row(row) * dim;
   float4 v[4], g[4];
   float ss = 0.0f;
 #pragma unroll
@@ -335,12 +335,6 @@ __global__ __launch_bounds__(256) void k_forecast_out(const ForecastOutDesc d) {
   if (!finite && d.nonfinite) *d.nonfinite = 1;
 }
 
-__global__ void k_gather_map(int* map, int v, int p, int ctx_p, int hp) {
-  const int t = blockIdx.x * 256 + threadIdx.x;
-  if (t >= v * hp) return;
-  map[t] = (t / hp) * p + ctx_p - 1 + (t % hp);
-}
-
 __global__ __launch_bounds__(256) void k_ar_shift(float* next, const float* ctx, const float* out, int v, int t_ctx,
                                                   int horizon, int nq, int q_idx) {
   const long long t = (long long)blockIdx.x * 256 + threadIdx.x;
@@ -412,15 +406,15 @@ void allow_dynamic_lds(const void* fn, std::atomic<uint64_t>& done) {
   done.fetch_or(bit, std::memory_order_release);
 }
 
-void launch_rmsnorm(const float* x, const float* scale, _Float16* out, const int* row_map, int rows, int dim,
+void launch_rmsnorm(const float* x, const float* scale, _Float16* out, const RowGather& gth, int rows, int dim,
                     hipStream_t s) {
   if (rows <= 0) return;
   if (!x || !scale || !out) throw Error(T0H_ERR_INVALID_ARG, "rmsnorm: null pointer");
   if (dim <= 0 || dim % 4) throw Error(T0H_ERR_UNSUPPORTED, "rmsnorm: dim must be a positive multiple of 4");
   if (dim <= 1024)
-    hipLaunchKernelGGL(k_rmsnorm_reg, dim3(blocks(rows, 4)), dim3(256), 0, s, x, scale, out, row_map, rows, dim);
+    hipLaunchKernelGGL(k_rmsnorm_reg, dim3(blocks(rows, 4)), dim3(256), 0, s, x, scale, out, gth, rows, dim);
   else
-    hipLaunchKernelGGL(k_rmsnorm, dim3(blocks(rows, 4)), dim3(256), 0, s, x, scale, out, row_map, rows, dim);
+    hipLaunchKernelGGL(k_rmsnorm, dim3(blocks(rows, 4)), dim3(256), 0, s, x, scale, out, gth, rows, dim);
   check_hip(hipGetLastError(), "k_rmsnorm launch");
 }
 
@@ -465,12 +459,6 @@ void launch_forecast_out(const ForecastOutDesc& d, hipStream_t s) {
   if (d.v <= 0 || d.hp <= 0) return;
   hipLaunchKernelGGL(k_forecast_out, dim3(blocks((long long)d.v * d.hp * d.ps, 256)), dim3(256), 0, s, d);
   check_hip(hipGetLastError(), "k_forecast_out launch");
-}
-
-void launch_gather_map(int* map, int v, int p, int ctx_p, int hp, hipStream_t s) {
-  if (v <= 0 || hp <= 0) return;
-  hipLaunchKernelGGL(k_gather_map, dim3(blocks((long long)v * hp, 256)), dim3(256), 0, s, map, v, p, ctx_p, hp);
-  check_hip(hipGetLastError(), "k_gather_map launch");
 }
 
 void launch_ar_shift(float* ctx_next, const float* ctx, const float* out, int v, int t_ctx, int horizon, int nq,

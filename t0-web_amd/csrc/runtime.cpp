@@ -627,8 +627,9 @@ void encode_and_layers(t0h_model* m, int v, int p, const PatchMeta& pm, float* t
   // RMSNorm split across the GEMMs either side of it (ops.rs:12-17): each residual
   // GEMM of the layers (wO, w2) also writes f16(x * g / 16) and per-row
   // partial sums of squares, and the consuming GEMM (QKV, SwiGLU) scales its output
-  // rows by 16 / sqrt(mean + eps).  Used below 1024 rows when every kernel involved
-  // supports it (one series, config 3: 0.597 -> 0.582 ms: 23 fewer launches); at
+  // rows by 16 / sqrt(mean + eps); the patch encoder's output GEMM produces layer 0's.
+  // Used below 1024 rows when every kernel involved supports it (one series,
+  // config 3: 0.597 -> 0.582 ms: 23 fewer launches); at
   // config 4 it measured 5 % slower (the producers' epilogues +40 us, the consumers'
   // per-tile wait for their rows' sums +24 us, against 68 us of norm launches per
   // layer), so larger windows keep each norm as its own launch.
@@ -666,7 +667,9 @@ void encode_and_layers(t0h_model* m, int v, int p, const PatchMeta& pm, float* t
     g.ssq_dim = E;
   };
 
-  // patch encoder residual block + type embedding (model.rs:199-207)
+  // patch encoder residual block + type embedding (model.rs:199-207); its output
+  // GEMM produces layer 0's norm when it can
+  bool enc_produces = false;
   {
     ProfScope ps_(m, "gemm_encoder");
     launch_gemm(gemm(m->enc.hid, pm.enc_in, 3 * ps, m->enc.hb, xn, m->enc.hid.n, M, EPI_STORE_F16, 1), s);
@@ -674,7 +677,10 @@ void encode_and_layers(t0h_model* m, int v, int p, const PatchMeta& pm, float* t
     rd.row_add = m->type_emb;
     rd.row_add_idx = pm.type_idx;
     launch_gemm(rd, s);
-    launch_gemm(gemm(m->enc.out, xn, m->enc.hid.n, m->enc.ob, x, E, M, EPI_RESID_F32), s);
+    GemmDesc eo = gemm(m->enc.out, xn, m->enc.hid.n, m->enc.ob, x, E, M, EPI_RESID_F32);
+    enc_produces = split && rownorm_producer_ok(eo);
+    if (enc_produces) produce(eo, m->layers[0].norm);
+    launch_gemm(eo, s);
   }
   if (trace_pe) download(m, trace_pe, x, (size_t)M * E);
 
@@ -701,36 +707,41 @@ void encode_and_layers(t0h_model* m, int v, int p, const PatchMeta& pm, float* t
   }
   for (size_t li = 0; li < m->layers.size(); ++li) {
     const Layer& L = m->layers[li];
-    if (!split || li == 0) {  // the encoder's output (F16 weights) has no split epilogue
+    if (!split || (li == 0 && !enc_produces)) {
       ProfScope ps_(m, "rmsnorm");
-      launch_rmsnorm(x, L.norm, xn, nullptr, M, E, s);
+      launch_rmsnorm(x, L.norm, xn, RowGather{}, M, E, s);
     }
     {
       ProfScope ps_(m, "gemm_qkv");
       GemmDesc g = gemm(L.qkv, xn, E, L.b_qkv, qkv, 3 * E, M, EPI_STORE_F16);
-      if (li > 0) consume(g);
+      if (li > 0 || enc_produces) consume(g);
       launch_gemm(g, s);
     }
     ad.q_norm = L.q_norm;
     ad.k_norm = L.k_norm;
     ad.rope_q = rope + li * 2 * (size_t)p * 128;
     ad.rope_k = ad.rope_q + (size_t)p * 128;
-    if (L.group) {
+    // One variate row: every query of a group layer has one key, itself (or,
+    // an all-PAD patch, uniform weights over the one row), so the attention
+    // output is the value row exactly and wO reads V in place.
+    const bool v_in_place = L.group && v == 1;
+    if (L.group && !v_in_place) {
       ProfScope ps_(m, "attn_group");
       launch_group_attention(ad, s);
-    } else {
+    } else if (!L.group) {
       ProfScope ps_(m, "attn_time");
       launch_time_attention(ad, s);
     }
     {
       ProfScope ps_(m, "gemm_wo_resid");
-      GemmDesc g = gemm(L.o, xn, E, L.b_o, x, E, M, EPI_RESID_F32);
+      GemmDesc g = v_in_place ? gemm(L.o, qkv + 2 * E, 3 * E, L.b_o, x, E, M, EPI_RESID_F32)
+                              : gemm(L.o, xn, E, L.b_o, x, E, M, EPI_RESID_F32);
       produce(g, L.mlp_norm);
       launch_gemm(g, s);
     }
     if (!split) {
       ProfScope ps_(m, "rmsnorm");
-      launch_rmsnorm(x, L.mlp_norm, xn, nullptr, M, E, s);
+      launch_rmsnorm(x, L.mlp_norm, xn, RowGather{}, M, E, s);
     }
     {
       ProfScope ps_(m, "gemm_w0_swiglu");
@@ -748,8 +759,8 @@ void encode_and_layers(t0h_model* m, int v, int p, const PatchMeta& pm, float* t
   }
 }
 
-// out_norm + decoder residual block on `rows` rows of x (gathered through map, or all).
-float* decode_rows(t0h_model* m, int rows, const int* map) {
+// out_norm + decoder residual block on `rows` rows of x (gathered per `gth`, or all).
+float* decode_rows(t0h_model* m, int rows, const RowGather& gth) {
   const t0h_config& c = m->mc.c;
   const int E = (int)c.embed_dim, nout = m->dec.out.n;
   hipStream_t s = m->stream;
@@ -758,7 +769,7 @@ float* decode_rows(t0h_model* m, int rows, const int* map) {
   _Float16* dh = ws_get<_Float16>(m, "dec_h", (size_t)rows * m->dec.hid.n);
   float* dout = ws_get<float>(m, "dec_out", (size_t)rows * nout);
   ProfScope ps_(m, "decoder");
-  launch_rmsnorm(x, m->out_norm, din, map, rows, E, s);
+  launch_rmsnorm(x, m->out_norm, din, gth, rows, E, s);
   launch_gemm(gemm(m->dec.hid, din, E, m->dec.hb, dh, m->dec.hid.n, rows, EPI_STORE_F16, 1), s);
   launch_gemm(gemm(m->dec.res, din, E, m->dec.rb, dout, nout, rows, EPI_STORE_F32), s);
   launch_gemm(gemm(m->dec.out, dh, m->dec.hid.n, m->dec.ob, dout, nout, rows, EPI_RESID_F32), s);
@@ -892,7 +903,6 @@ void forecast_window(t0h_model* m, const WindowRows& wr, float* d_out) {
   // every device buffer of the window is sized before the first upload or launch
   const PatchMeta pm = patch_buffers(m, v, p);
   reserve_forward(m, v, p, v * std::max(hp, 1));
-  int* map = ws_get<int>(m, "dec_map", (size_t)v * std::max(hp, 1));
   ws_get<int64_t>(m, "win_off", v);
   for (const char* n : {"win_len", "win_grp", "perm", "seg_begin", "seg_len"}) ws_get<int>(m, n, v);
   ws_get<float>(m, "rope", m->layers.size() * 2 * (size_t)p * 128);
@@ -928,8 +938,7 @@ void forecast_window(t0h_model* m, const WindowRows& wr, float* d_out) {
     }
     encode_and_layers(m, v, p, pm, nullptr, nullptr);
     if (hp == 0) return;
-    launch_gather_map(map, v, p, ctx_p, hp, s);
-    float* dout = decode_rows(m, v * hp, map);
+    float* dout = decode_rows(m, v * hp, RowGather{p, ctx_p, hp});
     ProfScope ps_(m, "forecast_out");
     ForecastOutDesc od;
     od.dec = dout;
@@ -1359,7 +1368,7 @@ int t0h_forward(t0h_model* m, const t0h_series* sr, float* out, size_t out_len, 
   ensure_rope(m, p);
   encode_and_layers(m, v, p, pm, trace_pe, trace_l0);
   const int M = v * p;
-  float* dout = decode_rows(m, M, nullptr);
+  float* dout = decode_rows(m, M, RowGather{});
   float* q = ws_get<float>(m, "out", (size_t)M * ps * nq);
   launch_quantile_head(dout, q, M * ps, 1, nq, m->stream);
   download(m, out, q, (size_t)M * ps * nq);

@@ -275,6 +275,16 @@ def test_medium_m_forward_epilogues(torch_cuda, t0hip, oracle, rng, qtype, epi, 
     check_forward_gemm(torch_cuda, t0hip, oracle, rng, qtype, 0, epi, m, k, n, sample=False)
 
 
+@pytest.mark.parametrize("epi", [0, 1, 2, 3])
+@pytest.mark.parametrize("m,k,n", [(66, 96, 768), (17, 32, 40), (300, 160, 72), (66, 768, 768), (200, 2048, 40),
+                                   (1000, 96, 520)])
+def test_medium_m_f16_weights(torch_cuda, t0hip, oracle, rng, epi, m, k, n):
+    """F16 weights on the medium-M kernel (the patch encoder and decoder at one series: K = 96 and
+    768): K % 64 == 32 (the upper lane half of the last 64-wide step is past K and contributes
+    zeros), a single 32-wide step, up to four steps per wave, ragged M and N."""
+    check_forward_gemm(torch_cuda, t0hip, oracle, rng, 1, 0, epi, m, k, n, sample=False)
+
+
 @pytest.mark.parametrize("qtype", [8, 2])
 @pytest.mark.parametrize("epi", [0, 1, 2, 3])
 @pytest.mark.parametrize("m,k,n", [(1023, 768, 96), (1024, 768, 96), (512, 768, 2304), (513, 768, 2304),
