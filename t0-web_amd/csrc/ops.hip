@@ -78,36 +78,6 @@ __global__ __launch_bounds__(256) void k_rmsnorm_reg(const float* x, const float
 }
 
 // ---- forecast window (data.rs:52-155 + lib.rs:208-236) ------------------------------
-struct Step {
-  float x;
-  int mask, group, type;
-};
-__device__ __forceinline__ Step window_step(const WindowDesc& w, int r, int s) {
-  Step st{0.0f, T0H_MASK_PAD, -1, -1};
-  if (s < w.pad_left) return st;  // left padding to a patch boundary (data.rs:112, 118-122)
-  const int c = s - w.pad_left;
-  const int g = w.group[r];
-  if (c < w.t_ctx) {
-    const int lead = w.t_ctx - w.len[r];  // ragged rows start late (lib.rs:215-216)
-    if (c < lead) return st;
-    const float x = w.ctx[w.src_off[r] + (c - lead)];
-    st.group = g;
-    st.type = T0H_VT_TARGET;
-    if (isnan(x)) {
-      st.mask = T0H_MASK_MISSING;  // data.rs:64-66
-    } else {
-      st.x = x;
-      st.mask = T0H_MASK_VALID;
-    }
-    return st;
-  }
-  // horizon and its right padding: WITHHELD target steps (data.rs:72-76, 136-144)
-  st.group = g;
-  st.type = T0H_VT_TARGET;
-  st.mask = T0H_MASK_WITHHELD;
-  return st;
-}
-
 // Rust 1.99 std f32::asinh: ln_1p(ax + ax / (hypot(1, 1/ax) + 1/ax)) with x's sign.
 __device__ __forceinline__ float rust_asinh(float x) {
   const float ax = fabsf(x);
@@ -174,16 +144,41 @@ __global__ __launch_bounds__(256) void k_prep_rows(const WindowDesc w, const Pat
   float* scv = xs + t;         // [t] scaled value
   float* pl = scv + t;         // [p] loc at patch end
   float* psc = pl + p;         // [p] scale at patch end
-  // [t] step masks: the later passes read them here instead of calling
-  // window_step again (a dependent global load per step; one row's patch
-  // metadata loop alone took about 20 us that way).  A step's group is the
+  // [t] step masks: the later passes read them here instead of rebuilding the
+  // window (a dependent global load per step; one row's patch metadata loop
+  // alone took about 20 us that way).  A step's group is the
   // row's and its type TARGET unless the step is PAD (group and type -1).
   unsigned char* smask = reinterpret_cast<unsigned char*>(psc + p);
 
-  for (int s = tid; s < t; s += 256) {
-    const Step stp = window_step(w, r, s);
-    xs[s] = stp.mask == T0H_MASK_VALID ? stp.x : NAN;
-    smask[s] = (unsigned char)stp.mask;
+  // Steps [0, pad_left) PAD | then t_ctx context steps: `lead` PAD (a ragged row
+  // starts late), the row's values (NaN = MISSING) | the horizon WITHHELD
+  // (data.rs:52-76, 110-155; lib.rs:215-216).  Eight steps a thread per batch,
+  // their loads issued before any is used.
+  {
+    const int lead = w.t_ctx - w.len[r];
+    const float* src = w.ctx + w.src_off[r] - lead - w.pad_left;  // value of step s at src[s]
+    for (int b = tid; b < t; b += 256 * 8) {
+      float xv[8];
+#pragma unroll
+      for (int u = 0; u < 8; ++u) {
+        const int s = b + 256 * u, c = s - w.pad_left;
+        xv[u] = s < t && c >= lead && c < w.t_ctx ? src[s] : 0.0f;
+      }
+#pragma unroll
+      for (int u = 0; u < 8; ++u) {
+        const int s = b + 256 * u, c = s - w.pad_left;
+        if (s >= t) break;
+        int mk;
+        if (c < 0 || (c < w.t_ctx && c < lead))
+          mk = T0H_MASK_PAD;
+        else if (c >= w.t_ctx)
+          mk = T0H_MASK_WITHHELD;
+        else
+          mk = isnan(xv[u]) ? T0H_MASK_MISSING : T0H_MASK_VALID;
+        xs[s] = mk == T0H_MASK_VALID ? xv[u] : NAN;
+        smask[s] = (unsigned char)mk;
+      }
+    }
   }
   __syncthreads();
   const int C = (t + 255) / 256;
@@ -236,8 +231,13 @@ __global__ __launch_bounds__(256) void k_prep_rows(const WindowDesc w, const Pat
   __syncthreads();
   const size_t m0 = (size_t)r * p;
   _Float16* enc = o.enc_in + m0 * 3 * ps;
-  for (int idx = tid; idx < p * 3 * ps; idx += 256) {
-    const int pi = idx / (3 * ps), f = idx % (3 * ps);
+  const int F = 3 * ps, dq = 256 / F, dr = 256 % F;
+  int pi = tid / F, f = tid % F;  // of idx, stepped by 256 without divisions
+  for (int idx = tid; idx < p * F; idx += 256, pi += dq, f += dr) {
+    if (f >= F) {
+      f -= F;
+      ++pi;
+    }
     float val;
     if (f < ps)
       val = scv[pi * ps + f];
@@ -249,12 +249,13 @@ __global__ __launch_bounds__(256) void k_prep_rows(const WindowDesc w, const Pat
   }
   const int g = w.group[r];
   for (int pi = tid; pi < p; pi += 256) {
+    // every non-PAD step of the window has the row's group and type TARGET, so the
+    // patch's first non-PAD step (mask.rs:12-28) gives those when there is one
+    bool any = false;
+#pragma unroll 8
+    for (int k = 0; k < ps; ++k) any |= smask[pi * ps + k] != T0H_MASK_PAD;
     PatchAcc acc;
-    for (int k = 0; k < ps; ++k) {
-      const int mk = smask[pi * ps + k];
-      const bool pad = mk == T0H_MASK_PAD;
-      acc.add(mk, pad ? -1 : g, pad ? -1 : T0H_VT_TARGET);
-    }
+    if (any) acc.add(T0H_MASK_VALID, g, T0H_VT_TARGET);
     write_patch_meta(o, m0 + pi, acc);
     if (o.patch_loc) {
       o.patch_loc[m0 + pi] = pl[pi];

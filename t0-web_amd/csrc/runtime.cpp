@@ -157,10 +157,12 @@ struct t0h_model {
   size_t noalloc_host_bytes = 0;
   hipEvent_t noalloc_ev = nullptr;
   bool noalloc_pending = false;
-  // Set to 1 on the device when a forecast's quantile logits are not finite (an
-  // f16 activation beyond +-65504 became inf, or the weights hold inf/NaN); lives
-  // at the end of the weights allocation.  `nonfinite_unread`: a device-output
-  // call may have set it since it was last read.
+  // Set to 1 by the device when a forecast's quantile logits are not finite (an
+  // f16 activation beyond +-65504 became inf, or the weights hold inf/NaN): an
+  // int in coherent pinned host memory (allocated at load), written by the kernel
+  // through its device address and read by the host after the stream drains.
+  // `nonfinite_unread`: a device-output call may have set it since it was read.
+  int* h_nonfinite = nullptr;
   int* d_nonfinite = nullptr;
   bool nonfinite_unread = false;
 };
@@ -396,8 +398,6 @@ void load_model(t0h_model* m, const uint8_t* bytes, size_t len) {
     off = align256(off + pl.bytes);
     place[n] = pl;
   }
-  const size_t flag_off = off;  // the non-finite flag (256 bytes, zero)
-  off += 256;
   std::vector<uint8_t> host(off, 0);
   for (auto& kv : place) {
     const Placement& pl = kv.second;
@@ -416,9 +416,8 @@ void load_model(t0h_model* m, const uint8_t* bytes, size_t len) {
     (void)hipGetLastError();
     throw Error(T0H_ERR_OOM, "device allocation for weights failed");
   }
-  m->weights_bytes = flag_off;
+  m->weights_bytes = off;
   hip_check(hipMemcpy(m->d_weights, host.data(), off, hipMemcpyHostToDevice), "hipMemcpy weights");
-  m->d_nonfinite = reinterpret_cast<int*>(m->d_weights + flag_off);
 
   auto mat = [&](const std::string& n) {
     const Placement& pl = place.at(n);
@@ -980,28 +979,45 @@ void check_out(size_t out_len, size_t want) {
     throw Error(T0H_ERR_INVALID_ARG, "output buffer holds " + std::to_string(out_len) + " floats, expected " + std::to_string(want));
 }
 
-// The non-finite flag around a host-output call: cleared first if a device-output
-// call may have set it, read back with the results (the caller synchronizes after).
+// The non-finite flag around a host-output call: if a device-output call may have
+// set it, the stream drains and it is cleared before this call's work.
 void numerics_begin(t0h_model* m) {
   if (!m->nonfinite_unread) return;
-  hip_check(hipMemsetAsync(m->d_nonfinite, 0, sizeof(int), m->stream), "hipMemsetAsync");
+  sync(m);
+  *static_cast<volatile int*>(m->h_nonfinite) = 0;
   m->nonfinite_unread = false;
 }
-void numerics_read(t0h_model* m, int* host_flag) { download(m, host_flag, m->d_nonfinite, 1); }
-void numerics_end(t0h_model* m, int host_flag);
-// Waits for a host-output call's results and raises T0H_ERR_NUMERIC if they are not finite.
-void finish_host_call(t0h_model* m) {
-  int nf = 0;
-  numerics_read(m, &nf);
-  sync(m);
-  numerics_end(m, nf);
-}
-void numerics_end(t0h_model* m, int host_flag) {
-  if (!host_flag) return;
-  hip_check(hipMemsetAsync(m->d_nonfinite, 0, sizeof(int), m->stream), "hipMemsetAsync");
-  sync(m);
+// After the stream has drained: raises T0H_ERR_NUMERIC (clearing the flag) if set.
+void numerics_end(t0h_model* m) {
+  volatile int* f = m->h_nonfinite;
+  if (!*f) return;
+  *f = 0;
   throw Error(T0H_ERR_NUMERIC,
               "forecast produced non-finite model outputs: an f16 activation exceeded 65504, or the weights are not finite");
+}
+// A host-output call's end: its n results at d_out come back through pinned
+// staging (one asynchronous copy), the stream drains, the numeric flag is checked.
+void finish_host_call(t0h_model* m, float* out, const float* d_out, size_t n) {
+  const size_t bytes = n * sizeof(float);
+  if (bytes) {
+    Stage& st = m->ws.stages["results"];
+    if (st.cap < bytes) {
+      if (st.p) hip_check(hipHostFree(st.p), "hipHostFree");
+      st.p = nullptr;
+      st.cap = 0;
+      if (hipHostMalloc(&st.p, bytes + bytes / 4, hipHostMallocDefault) != hipSuccess) {
+        (void)hipGetLastError();
+        throw Error(T0H_ERR_OOM, "pinned host allocation failed");
+      }
+      st.cap = bytes + bytes / 4;
+    }
+    hip_check(hipMemcpyAsync(st.p, d_out, bytes, hipMemcpyDeviceToHost, m->stream), "hipMemcpyAsync D2H");
+    sync(m);
+    std::memcpy(out, st.p, bytes);
+  } else {
+    sync(m);
+  }
+  numerics_end(m);
 }
 
 // forecast_rollout helpers (quantile.rs:16-76)
@@ -1090,8 +1106,7 @@ void forecast_host(t0h_model* m, const float* ctx, size_t v, size_t t_ctx, size_
   }
   float* d_out = ws_get<float>(m, "out", std::max<size_t>(1, v * horizon * nq));
   forecast_window(m, wr, d_out);
-  download(m, out, d_out, v * horizon * nq);
-  finish_host_call(m);
+  finish_host_call(m, out, d_out, v * horizon * nq);
 }
 
 void forecast_batch_host(t0h_model* m, const float* ctx, size_t n, size_t t_ctx, size_t horizon, size_t chunk,
@@ -1114,8 +1129,7 @@ void forecast_batch_host(t0h_model* m, const float* ctx, size_t n, size_t t_ctx,
     }
     forecast_window(m, wr, d_out + start * horizon * nq);
   }
-  download(m, out, d_out, n * horizon * nq);
-  finish_host_call(m);
+  finish_host_call(m, out, d_out, n * horizon * nq);
 }
 
 }  // namespace t0h
@@ -1202,7 +1216,19 @@ int t0h_model_load_gguf(t0h_ctx* ctx, const uint8_t* bytes, size_t len, t0h_mode
       throw Error(T0H_ERR_OOM, "pinned host allocation failed");
     }
     hip_check(hipEventCreateWithFlags(&m->noalloc_ev, hipEventDisableTiming), "hipEventCreate");
+    void* flag = nullptr;
+    if (hipHostMalloc(&flag, 64, hipHostMallocCoherent) != hipSuccess) {
+      (void)hipGetLastError();
+      throw Error(T0H_ERR_OOM, "pinned host allocation failed");
+    }
+    m->h_nonfinite = static_cast<int*>(flag);
+    *m->h_nonfinite = 0;
+    void* dflag = nullptr;
+    hip_check(hipHostGetDevicePointer(&dflag, flag, 0), "hipHostGetDevicePointer");
+    m->d_nonfinite = static_cast<int*>(dflag);
   } catch (...) {
+    if (m->h_nonfinite) (void)hipHostFree(m->h_nonfinite);
+    if (m->noalloc_ev) (void)hipEventDestroy(m->noalloc_ev);
     if (m->noalloc_host) (void)hipHostFree(m->noalloc_host);
     if (m->d_weights) (void)hipFree(m->d_weights);
     (void)hipStreamDestroy(m->stream);
@@ -1231,6 +1257,7 @@ void t0h_model_destroy(t0h_model* m) {
   for (hipEvent_t e : m->prof.spare) (void)hipEventDestroy(e);
   if (m->noalloc_host) (void)hipHostFree(m->noalloc_host);
   if (m->noalloc_ev) (void)hipEventDestroy(m->noalloc_ev);
+  if (m->h_nonfinite) (void)hipHostFree(m->h_nonfinite);
   if (m->d_weights) (void)hipFree(m->d_weights);
   (void)hipStreamDestroy(m->stream);
   delete m;
@@ -1434,8 +1461,7 @@ int t0h_forecast_batch_rows_chunked(t0h_model* m, const float* contexts, const s
     }
     forecast_window(m, wr, d_out + start * horizon * nq);
   }
-  download(m, out, d_out, n * horizon * nq);
-  finish_host_call(m);
+  finish_host_call(m, out, d_out, n * horizon * nq);
   API_END
 }
 
@@ -1464,8 +1490,7 @@ int t0h_forecast_grouped(t0h_model* m, const float* contexts, const int64_t* row
   grouped_rows(wr, row_group, n_rows, t_ctx);
   float* d_out = ws_get<float>(m, "out", std::max<size_t>(1, n_rows * horizon * nq));
   forecast_window(m, wr, d_out);
-  download(m, out, d_out, n_rows * horizon * nq);
-  finish_host_call(m);
+  finish_host_call(m, out, d_out, n_rows * horizon * nq);
   API_END
 }
 
@@ -1528,11 +1553,9 @@ int t0h_model_check_numerics(t0h_model* m) {
   API_BEGIN
   require(m, "t0h_model_check_numerics: NULL model");
   bind_device(m);
-  int nf = 0;
-  numerics_read(m, &nf);
   sync(m);
   m->nonfinite_unread = false;
-  numerics_end(m, nf);
+  numerics_end(m);
   API_END
 }
 
@@ -1562,8 +1585,7 @@ int t0h_forecast_grouped_ar(t0h_model* m, const float* contexts, const int64_t* 
     launch_ar_shift(ctx_b, ctx_a, step_out, (int)n_rows, (int)t_ctx, (int)horizon, (int)nq, qi, m->stream);
     std::swap(ctx_a, ctx_b);
   }
-  download(m, out, result, n_rows * steps * horizon * nq);
-  finish_host_call(m);
+  finish_host_call(m, out, result, n_rows * steps * horizon * nq);
   API_END
 }
 
