@@ -214,10 +214,15 @@ __device__ __forceinline__ void tile_bias1(const GemmDesc& d, int lane, int cbas
 // each of the tile's rows (rs[32 i + r] for row row_base + 32 i + r), applied to
 // the accumulators before the bias; 2 producer (EPI_RESID_F32, vector stores,
 // N % 32 == 0): the residual rows' f16 norm input and partial sums of squares.
-template <int EPI, int TI, int TJ, bool PRE = false, int RN = 0>
+// PREO (TI == 1, one 32-column group, vector stores): the caller loaded the
+// residual's old rows (old_pre, as load_old below) and the producer's norm scales
+// (g_pre, the four columns of each chunk) before its main loop.
+template <int EPI, int TI, int TJ, bool PRE = false, int RN = 0, bool PREO = false>
 __device__ __forceinline__ void store_tile(const GemmDesc& d, floatx16 (&acc)[TI][TJ], float* smemf, int wave,
                                            int lane, int row_base, int cbase, float pre0 = 0.0f,
-                                           float pre1 = 0.0f, const float* rs = nullptr) {
+                                           float pre1 = 0.0f, const float* rs = nullptr,
+                                           const float4* old_pre = nullptr, const float4* g_pre = nullptr) {
+  static_assert(!PREO || (TI == 1 && TJ == 1 && EPI == EPI_RESID_F32), "preloaded rows: one residual slice");
   static_assert(RN != 1 || EPI != EPI_RESID_F32, "a residual epilogue is not a norm consumer");
   static_assert(RN != 2 || EPI == EPI_RESID_F32, "only a residual epilogue produces the norm");
   constexpr bool SWI = EPI == EPI_SWIGLU_F16;
@@ -328,7 +333,12 @@ __device__ __forceinline__ void store_tile(const GemmDesc& d, floatx16 (&acc)[TI
       }
     }
   };
-  if (RES2 && vec_ok) load_old(0, yo[0]);
+  if constexpr (PREO) {
+#pragma unroll
+    for (int t = 0; t < NT; ++t) yo[0][t] = old_pre[t];
+  } else if (RES2 && vec_ok) {
+    load_old(0, yo[0]);
+  }
   // Each wave stages into and reads back from its own region, and a wave's
   // LDS operations complete in order: no barrier is needed.
 #pragma unroll
@@ -381,7 +391,7 @@ __device__ __forceinline__ void store_tile(const GemmDesc& d, floatx16 (&acc)[TI
           const float4 nx = make_float4(old.x + v.x, old.y + v.y, old.z + v.z, old.w + v.w);
           *reinterpret_cast<float4*>(static_cast<float*>(d.y) + o) = nx;
           if constexpr (RN == 2) {  // split RMSNorm producer (N % 32 == 0: a 32-column group's 8 lanes are all here)
-            const float4 g4 = *reinterpret_cast<const float4*>(d.norm_g + col);
+            const float4 g4 = PREO ? g_pre[t] : *reinterpret_cast<const float4*>(d.norm_g + col);
             const half4 hn = {(_Float16)(nx.x * g4.x * RN_SCALE), (_Float16)(nx.y * g4.y * RN_SCALE),
                               (_Float16)(nx.z * g4.z * RN_SCALE), (_Float16)(nx.w * g4.w * RN_SCALE)};
             *reinterpret_cast<half4*>(d.norm_out + (size_t)row * N + col) = hn;
@@ -1535,6 +1545,25 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2))) void k
         }
       }
   }
+  // The epilogue waves' bias, and for a residual slice its old rows and the
+  // producer's norm scales, loaded with the operands (one group of 32 columns,
+  // 16-byte stores), so the epilogue starts without a memory round trip.
+  constexpr bool PREB = TJ == 1, PREO = TJ == 1 && TI == 1 && EPI == EPI_RESID_F32 && KR <= 4;
+  const bool preo = PREO && (d.ldy & 3) == 0 && (N & 3) == 0;
+  float pb0 = 0.0f, pb1 = 0.0f;
+  float4 pold[PREO ? 4 : 1], pg[PREO ? 4 : 1];
+  if (PREB && wave < TI) tile_bias1<EPI>(d, lane, tn * W, pb0, pb1);
+  if (PREO && preo && wave == 0) {
+#pragma unroll
+    for (int t = 0; t < 4; ++t) {
+      const int idx = t * 64 + lane, row = m0 + idx / 8, col = tn * W + (idx % 8) * 4;
+      const bool in = row < M && col < N;
+      pold[t] = in ? *reinterpret_cast<const float4*>(static_cast<const float*>(d.y) + (size_t)row * d.ldy + col)
+                   : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+      if constexpr (RN == 2) pg[t] = col < N ? *reinterpret_cast<const float4*>(d.norm_g + col)
+                                             : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+    }
+  }
   half8 af[KR][4][TI];
 #pragma unroll
   for (int i = 0; i < TI; ++i) {
@@ -1606,8 +1635,12 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2))) void k
         sum[0][j][4 * q + 3] += v.w;
       }
   // staging after the partials (other slices may still be reading them)
-  store_tile<EPI, 1, TJ, false, RN>(d, sum, red + nw * TI * TJ * 16 * 64, wave, lane, m0 + 32 * wave, tn * W,
-                                    0.0f, 0.0f, rsc_s + 32 * wave);
+  float* const stage = red + nw * TI * TJ * 16 * 64;
+  if (PREO && preo)
+    store_tile<EPI, 1, TJ, PREB, RN, PREO>(d, sum, stage, wave, lane, m0 + 32 * wave, tn * W, pb0, pb1,
+                                           rsc_s + 32 * wave, pold, pg);
+  else
+    store_tile<EPI, 1, TJ, PREB, RN>(d, sum, stage, wave, lane, m0 + 32 * wave, tn * W, pb0, pb1, rsc_s + 32 * wave);
 }
 
 // ---------------------------------------------------------------------------
