@@ -42,13 +42,13 @@ __host__ __device__ inline int round_up(int x, int m) { return (x + m - 1) / m *
 // pairs land in distinct banks up to a 2-way conflict.
 __host__ __device__ inline int vt_stride(int P32) { return P32 + 4; }
 
-// LDS of one (row, head) workgroup: Ks [P16][LDH] f16 keys after norm + RoPE
-// (rows >= p zero) | Vt [HD][LDV] f16 values by key pairs (keys >= p zero) |
+// LDS of one (row, head) workgroup: Ks [P16 + 1][LDH] f16 keys after norm + RoPE
+// (rows >= p zero; row P16 takes the key items past the window) | Vt [HD][LDV] f16 values by key pairs (keys >= p zero) |
 // Os [TA_WAVES][16][LDH] per-wave output staging | Kg [P32] int key group if
 // attendable, -2 if not, -4 past the window.
 size_t time_attn_lds(int p) {
   const int P16 = round_up(p, 16), P32 = round_up(p, 32);
-  return (size_t)P16 * LDH * 2 + (size_t)HD * vt_stride(P32) * 2 + (size_t)TA_WAVES * 16 * LDH * 2 + (size_t)P32 * 4;
+  return (size_t)(P16 + 1) * LDH * 2 + (size_t)HD * vt_stride(P32) * 2 + (size_t)TA_WAVES * 16 * LDH * 2 + (size_t)P32 * 4;
 }
 
 __device__ __forceinline__ void unpack8(uint4 u, float* x) {
@@ -82,12 +82,19 @@ __device__ __forceinline__ void load_f8(const float* t, float* a) {
 // rotated in registers; S^T = K Q^T and O = P V on v_mfma_f32_16x16x32_f16 with
 // the tile's scores in registers; O is staged through the wave's LDS region and
 // stored in 16-byte row chunks.
-template <int MAXKT>
+//
+// LAT (few (row, head) pairs, so the chain of memory round trips of one
+// workgroup is the kernel's time): rows past the window are loaded from a
+// clamped row and discarded where used instead of skipped under a branch, and
+// the key tables are prefetched two items ahead, so a workgroup waits about
+// once before its barrier.  With many pairs the other workgroups on the CU hide
+// those round trips and the extra loads would only cost issue slots.
+template <int MAXKT, bool LAT>
 __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(MAXKT <= 8 ? 4 : 3))) void k_time_attn(const AttnDesc d) {
   extern __shared__ __align__(16) _Float16 sm[];
   const int p = d.p, P16 = round_up(p, 16), P32 = round_up(p, 32), LDV = vt_stride(P32);
   _Float16* Ks = sm;
-  _Float16* Vt = Ks + P16 * LDH;
+  _Float16* Vt = Ks + (P16 + 1) * LDH;  // Ks row P16: where key items past the window are written
   _Float16* Os = Vt + HD * LDV;
   int* Kg = reinterpret_cast<int*>(Os + TA_WAVES * 16 * LDH);
 
@@ -107,58 +114,144 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(MAXKT <= 8 
     const int j = (k >> 1) * 2 * NW + ((k & 1) ? 2 * NW - 1 - wv : wv);
     return j < nqt ? nqt - 1 - j : -1;
   };
+  // LAT: loads whose row may be past the window read a clamped row instead and the
+  // value is discarded where it is used: a load under a branch makes the
+  // compiler wait for it inside the branch, one memory round trip each.
   auto load_q = [&](int qt, uint4& a, uint4& b) {
-    const int qi = qt * 16 + (lane & 15);
-    a = b = make_uint4(0, 0, 0, 0);
-    if (qt >= 0 && qi < p) {
+    if constexpr (LAT) {
+      const int qi = min(max(qt, 0) * 16 + (lane & 15), p - 1);
       a = *reinterpret_cast<const uint4*>(qb + (size_t)qi * ld + part * 8);
       b = *reinterpret_cast<const uint4*>(qb + (size_t)qi * ld + 32 + part * 8);
+    } else {
+      const int qi = qt * 16 + (lane & 15);
+      a = b = make_uint4(0, 0, 0, 0);
+      if (qt >= 0 && qi < p) {
+        a = *reinterpret_cast<const uint4*>(qb + (size_t)qi * ld + part * 8);
+        b = *reinterpret_cast<const uint4*>(qb + (size_t)qi * ld + 32 + part * 8);
+      }
     }
   };
 
   // Key phase: all of a thread's k / v loads are issued before any is consumed.
-  constexpr int NK = MAXKT / 2, NV = MAXKT / 4;  // items per 8-lane group at the largest window
+  constexpr int NK = MAXKT / 2, NV = (MAXKT + 3) / 4;  // items per 8-lane group at the largest window
   const int d0 = (tid & 7) * 8, g8 = tid >> 3;
+  // (LAT: rows past the window load row p - 1; keys and values past it are zeroed where stored)
   uint4 kx[NK], vx[NV][2];
 #pragma unroll
   for (int it = 0; it < NK; ++it) {
     const int i = g8 + 32 * it;
-    kx[it] = i < p ? *reinterpret_cast<const uint4*>(qb + E + (size_t)i * ld + d0) : make_uint4(0, 0, 0, 0);
+    if constexpr (LAT)
+      kx[it] = *reinterpret_cast<const uint4*>(qb + E + (size_t)min(i, p - 1) * ld + d0);
+    else
+      kx[it] = i < p ? *reinterpret_cast<const uint4*>(qb + E + (size_t)i * ld + d0) : make_uint4(0, 0, 0, 0);
   }
 #pragma unroll
   for (int it = 0; it < NV; ++it) {
     const int i = 2 * (g8 + 32 * it);
-    const _Float16* src = qb + 2 * E + (size_t)i * ld + d0;
-    vx[it][0] = i < p ? *reinterpret_cast<const uint4*>(src) : make_uint4(0, 0, 0, 0);
-    vx[it][1] = i + 1 < p ? *reinterpret_cast<const uint4*>(src + ld) : make_uint4(0, 0, 0, 0);
+    const _Float16* src = qb + 2 * E + d0;
+    if constexpr (LAT) {
+      vx[it][0] = *reinterpret_cast<const uint4*>(src + (size_t)min(i, p - 1) * ld);
+      vx[it][1] = *reinterpret_cast<const uint4*>(src + (size_t)min(i + 1, p - 1) * ld);
+    } else {
+      vx[it][0] = i < p ? *reinterpret_cast<const uint4*>(src + (size_t)i * ld) : make_uint4(0, 0, 0, 0);
+      vx[it][1] = i + 1 < p ? *reinterpret_cast<const uint4*>(src + (size_t)(i + 1) * ld) : make_uint4(0, 0, 0, 0);
+    }
   }
+  // the row's FUTURE flag through the dword holding it: a scalar load, where a
+  // byte load would be a vector load waited for to make it uniform (the fut
+  // array is a workspace buffer with at least v / 4 bytes of slack after it)
+  const uint32_t futw = *reinterpret_cast<const uint32_t*>(d.fut + (r & ~3));
+  const bool fut = ((futw >> (8 * (r & 3))) & 0xffu) != 0;
   uint4 qa, qc;
   load_q(tile_at(0), qa, qc);
-  for (int i = tid; i < P32; i += blockDim.x) Kg[i] = i >= p ? -4 : d.att[row0 + i] ? d.grp[row0 + i] : -2;
+  // key groups (P32 <= 256: one key a thread), stored after the key phase
+  const int kgi = min(tid, p - 1);
+  const int kg_at = d.att[row0 + kgi], kg_g = d.grp[row0 + kgi];
+  if constexpr (LAT) {
+    // the k table rows of key items it + 1 and it + 2 are in flight while item it is rotated
+    float ka[3][8], kb[3][8];
+    auto load_kt = [&](int it, int buf) {
+      const int i = min(g8 + 32 * it, p - 1);
+      load_f8(d.rope_k + (size_t)i * 128 + d0, ka[buf]);
+      load_f8(d.rope_k + (size_t)i * 128 + 64 + d0, kb[buf]);
+    };
+    load_kt(0, 0);
+    if (NK > 1) load_kt(1, 1);
+    // scheduling fences keep the machine scheduler from moving the table loads
+    // down to their uses (one round trip per item)
+    __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
-  for (int it = 0; it < NK; ++it) {
-    const int i = g8 + 32 * it;
-    if (i >= P16) break;
-    float x[8];
-    unpack8(kx[it], x);
-    float ss = 0.0f;
+    for (int it = 0; it < NK; ++it) {  // every item (no early exit: the loads stay where issued)
+      const int i = g8 + 32 * it;
+      if (it + 2 < NK) load_kt(it + 2, (it + 2) % 3);
+      __builtin_amdgcn_sched_barrier(0);
+      float x[8];
+      unpack8(kx[it], x);
+      float ss = 0.0f;
 #pragma unroll
-    for (int e = 0; e < 8; ++e) ss += x[e] * x[e];
-    ss = lane_sum8(ss);
-    half8 o = {};
-    if (i < p) {
-      float a[8], b[8];
-      load_f8(d.rope_k + (size_t)i * 128 + d0, a);
-      load_f8(d.rope_k + (size_t)i * 128 + 64 + d0, b);
-      o = rotate8(x, a, b, 1.0f / sqrtf(ss / (float)HD + 1e-8f));
+      for (int e = 0; e < 8; ++e) ss += x[e] * x[e];
+      ss = lane_sum8(ss);
+      // computed for every item (a clamped row past the window) and then zeroed, so the
+      // compiler keeps the table loads where they are issued
+      half8 o = rotate8(x, ka[it % 3], kb[it % 3], 1.0f / sqrtf(ss / (float)HD + 1e-8f));
+      if (i >= p) o = (half8){};
+      // (an unconditional store: under a branch the compiler would move the item's
+      // table loads into it, after the previous item's wait)
+      *reinterpret_cast<uint4*>(Ks + min(i, P16) * LDH + d0) = __builtin_bit_cast(uint4, o);
     }
-    *reinterpret_cast<uint4*>(Ks + i * LDH + d0) = __builtin_bit_cast(uint4, o);
+  } else {
+#pragma unroll
+    for (int it = 0; it < NK; ++it) {
+      const int i = g8 + 32 * it;
+      if (i >= P16) break;
+      float x[8];
+      unpack8(kx[it], x);
+      float ss = 0.0f;
+#pragma unroll
+      for (int e = 0; e < 8; ++e) ss += x[e] * x[e];
+      ss = lane_sum8(ss);
+      half8 o = {};
+      if (i < p) {
+        float a[8], b[8];
+        load_f8(d.rope_k + (size_t)i * 128 + d0, a);
+        load_f8(d.rope_k + (size_t)i * 128 + 64 + d0, b);
+        o = rotate8(x, a, b, 1.0f / sqrtf(ss / (float)HD + 1e-8f));
+      }
+      *reinterpret_cast<uint4*>(Ks + i * LDH + d0) = __builtin_bit_cast(uint4, o);
+    }
   }
+  // A query tile's rows of the q table (norm scale x rotation x xpos scale);
+  // the next tile's are loaded after this tile's PV products, so they arrive
+  // during the output stores instead of at the head of the tile.
+  float ta[16], tb[16];
+  auto load_t = [&](int qt2) {
+    if constexpr (LAT) {
+      const int q2 = min(max(qt2, 0) * 16 + (lane & 15), p - 1);
+      const float* t = d.rope_q + (size_t)q2 * 128 + part * 8;
+      load_f8(t, ta);
+      load_f8(t + 32, ta + 8);
+      load_f8(t + 64, tb);
+      load_f8(t + 96, tb + 8);
+    } else {
+      const int q2 = qt2 * 16 + (lane & 15);
+      if (qt2 >= 0 && q2 < p) {
+        const float* t = d.rope_q + (size_t)q2 * 128 + part * 8;
+        load_f8(t, ta);
+        load_f8(t + 32, ta + 8);
+        load_f8(t + 64, tb);
+        load_f8(t + 96, tb + 8);
+      }
+    }
+  };
+  if constexpr (LAT) load_t(tile_at(0));  // in flight during the value transposition and the barrier
 #pragma unroll
   for (int it = 0; it < NV; ++it) {
     const int i = 2 * (g8 + 32 * it);
     if (i >= P32) break;
-    const half8 hv = __builtin_bit_cast(half8, vx[it][0]), hw = __builtin_bit_cast(half8, vx[it][1]);
+    // (selects of values: a select between two named arrays' elements would put
+    // them in private memory)
+    const half8 hv = __builtin_bit_cast(half8, i < p ? vx[it][0] : make_uint4(0, 0, 0, 0)),
+                hw = __builtin_bit_cast(half8, i + 1 < p ? vx[it][1] : make_uint4(0, 0, 0, 0));
     uint32_t* vt2 = reinterpret_cast<uint32_t*>(Vt);
 #pragma unroll
     for (int e = 0; e < 8; ++e) {
@@ -166,25 +259,11 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(MAXKT <= 8 
       vt2[((d0 + e) * LDV + i) >> 1] = __builtin_bit_cast(uint32_t, pr);
     }
   }
+  if (tid < P32) Kg[tid] = tid >= p ? -4 : kg_at ? kg_g : -2;
   __syncthreads();
+  if constexpr (!LAT) load_t(tile_at(0));
 
-  const bool fut = d.fut[r] != 0;
   _Float16* ost = Os + wave * 16 * LDH;
-  // A query tile's rows of the q table (norm scale x rotation x xpos scale);
-  // the next tile's are loaded after this tile's PV products, so they arrive
-  // during the output stores instead of at the head of the tile.
-  float ta[16], tb[16];
-  auto load_t = [&](int qt2) {
-    const int q2 = qt2 * 16 + (lane & 15);
-    if (qt2 >= 0 && q2 < p) {
-      const float* t = d.rope_q + (size_t)q2 * 128 + part * 8;
-      load_f8(t, ta);
-      load_f8(t + 32, ta + 8);
-      load_f8(t + 64, tb);
-      load_f8(t + 96, tb + 8);
-    }
-  };
-  load_t(tile_at(0));
   for (int k = 0;; ++k) {
     const int qt = tile_at(k);
     if (qt < 0) break;
@@ -199,10 +278,10 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(MAXKT <= 8 
     for (int e = 0; e < 16; ++e) ss += x[e] * x[e];
     ss = rows_sum(ss);
     half8 bq0 = {}, bq1 = {};
-    if (qi < p) {
-      const float inv = 1.0f / sqrtf(ss / (float)HD + 1e-8f);
-      bq0 = rotate8(x, ta, tb, inv);
-      bq1 = rotate8(x + 8, ta + 8, tb + 8, inv);
+    if (LAT || qi < p) {  // (LAT: rows past the window hold clamped data, never stored)
+      const float qinv = 1.0f / sqrtf(ss / (float)HD + 1e-8f);
+      bq0 = rotate8(x, ta, tb, qinv);
+      bq1 = rotate8(x + 8, ta + 8, tb + 8, qinv);
     }
     qa = na;
     qc = nc;
@@ -678,11 +757,19 @@ void check_common(const AttnDesc& d) {
     throw Error(T0H_ERR_UNSUPPORTED, "attention: head_dim must be 64 (embed_dim = 64 * num_heads)");
 }
 
+template <int MAXKT, bool LAT>
+void run_time_attn_k(const AttnDesc& d, size_t lds, hipStream_t s) {
+  static std::atomic<uint64_t> lds_set{0};  // per instantiation
+  allow_dynamic_lds(reinterpret_cast<const void*>(&k_time_attn<MAXKT, LAT>), lds_set);
+  hipLaunchKernelGGL((k_time_attn<MAXKT, LAT>), dim3(d.v * d.heads * d.qsplit), dim3(TA_WAVES * 64), lds, s, d);
+}
+// Latency-bound launches (query tiles split over workgroups: few pairs) take the LAT kernel.
 template <int MAXKT>
 void run_time_attn(const AttnDesc& d, size_t lds, hipStream_t s) {
-  static std::atomic<uint64_t> lds_set{0};  // per instantiation
-  allow_dynamic_lds(reinterpret_cast<const void*>(&k_time_attn<MAXKT>), lds_set);
-  hipLaunchKernelGGL(k_time_attn<MAXKT>, dim3(d.v * d.heads * d.qsplit), dim3(TA_WAVES * 64), lds, s, d);
+  if (d.qsplit > 1)
+    run_time_attn_k<MAXKT, true>(d, lds, s);
+  else
+    run_time_attn_k<MAXKT, false>(d, lds, s);
 }
 
 }  // namespace
@@ -708,10 +795,16 @@ void launch_time_attention(const AttnDesc& d, hipStream_t s) {
   AttnDesc dd = d;
   const int nqt = round_up(d.p, 16) / 16, pairs = d.v * d.heads;
   dd.qsplit = std::max(1, std::min(nqt, 256 / std::max(1, pairs)));
+  // (instances close to the window: every key item of an instance is loaded and
+  // rotated, rows past the window from a clamped row)
   if (kt <= 4)
     run_time_attn<4>(dd, lds, s);
+  else if (kt <= 6)
+    run_time_attn<6>(dd, lds, s);
   else if (kt <= 8)
     run_time_attn<8>(dd, lds, s);
+  else if (kt <= 10)
+    run_time_attn<10>(dd, lds, s);
   else if (kt <= 12)
     run_time_attn<12>(dd, lds, s);
   else

@@ -1986,6 +1986,18 @@ __global__ __launch_bounds__(64 * MF_WAVES) void k_gemv_mf(const GemmDesc d) {
   };
   constexpr int STEP = MF_WAVES * MF_CH;
   load_batch(wave, ops[0]);
+  // the output threads' bias (and old residual value), loaded with the first batch
+  const int m = tid >> 4, jj = tid & 15;
+  const int col = c0 + jj;
+  const bool outp = tid < 256 && m < M && (SWI ? jj < 8 : true) && col < N;
+  float pb = 0.0f, pb2 = 0.0f, py = 0.0f;
+  if (outp) {
+    if (d.bias) {
+      pb = d.bias[col];
+      if constexpr (SWI) pb2 = d.bias[N + col];
+    }
+    if constexpr (EPI == EPI_RESID_F32) py = static_cast<const float*>(d.y)[(size_t)m * d.ldy + col];
+  }
   int kb0 = wave;
   for (; kb0 + STEP < KB; kb0 += 2 * STEP) {  // pairs of batches: the buffers alternate
     load_batch(kb0 + STEP, ops[1]);
@@ -1998,29 +2010,22 @@ __global__ __launch_bounds__(64 * MF_WAVES) void k_gemv_mf(const GemmDesc d) {
 #pragma unroll
   for (int r = 0; r < 4; ++r) red[wave][4 * c + r][j] = acc[r];
   __syncthreads();
-  if (tid >= 256) return;
-  const int m = tid >> 4, jj = tid & 15;
-  if (m >= M) return;
+  if (!outp) return;
   float v = 0.0f;
 #pragma unroll
   for (int w = 0; w < MF_WAVES; ++w) v += red[w][m][jj];
   if constexpr (SWI) {
-    const int u = c0 + jj;
-    if (jj >= 8 || u >= N) return;
     float up = 0.0f;
 #pragma unroll
     for (int w = 0; w < MF_WAVES; ++w) up += red[w][m][jj + 8];
-    const float g = v + (d.bias ? d.bias[u] : 0.0f), uu = up + (d.bias ? d.bias[N + u] : 0.0f);
-    static_cast<_Float16*>(d.y)[(size_t)m * d.ldy + u] = (_Float16)(silu(g) * uu);
+    const float g = v + pb, uu = up + pb2;
+    static_cast<_Float16*>(d.y)[(size_t)m * d.ldy + col] = (_Float16)(silu(g) * uu);
   } else {
-    const int n = c0 + jj;
-    if (n >= N) return;
-    v += d.bias ? d.bias[n] : 0.0f;
+    v += pb;
     if (d.relu) v = fmaxf(v, 0.0f);
-    const size_t o = (size_t)m * d.ldy + n;
+    const size_t o = (size_t)m * d.ldy + col;
     if constexpr (EPI == EPI_RESID_F32) {
-      float* y = static_cast<float*>(d.y) + o;
-      *y = *y + v;
+      static_cast<float*>(d.y)[o] = py + v;
     } else if constexpr (EPI == EPI_STORE_F32) {
       static_cast<float*>(d.y)[o] = v;
     } else {
