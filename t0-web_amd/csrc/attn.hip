@@ -645,13 +645,14 @@ __global__ __launch_bounds__(256) void k_group_attn(const AttnDesc d) {
   *reinterpret_cast<uint4*>(d.out + m * E + h * HD + d0) = __builtin_bit_cast(uint4, hv);
 }
 
-// Group attention for segments of 5 to MAXG rows (one row group's variates
-// at one patch): the same 8-lane (query row, head) mapping and arithmetic as
-// k_group_attn, but the segment's permutation entries, then every key row's
-// group id and k / v chunks are loaded before the first score, so a query
-// waits for two load latencies instead of three per key; the softmax is taken
-// over the scores held in registers.  (For shorter segments the generic
-// kernel's higher occupancy measured faster.)
+// Group attention for segments of up to MAXG rows (one row group's variates at
+// one patch): the same 8-lane (query row, head) mapping and arithmetic as
+// k_group_attn, but with three memory round trips a query whatever the segment
+// length: the query row, its group and its segment; the segment's permutation
+// entries; every key row's group id and k / v chunks.  Entries past the segment
+// read its last row (clamped, no branch: a load under a branch is waited for
+// inside it) and are excluded from the softmax, taken over the scores held in
+// registers.
 template <int MAXG>
 __global__ __launch_bounds__(256) void k_group_attn_seg(const AttnDesc d) {
   const int H = d.heads, E = d.E, p = d.p, v = d.v, ld = 3 * E;
@@ -661,9 +662,71 @@ __global__ __launch_bounds__(256) void k_group_attn_seg(const AttnDesc d) {
   const int h = (int)(task % H);
   const long long m = task / H;
   const int r = (int)(m / p), pi = (int)(m % p);
-  const int gq = d.grp[m];
   const _Float16* col = d.qkv + (size_t)h * HD + d0;
+  const int gq = d.grp[m];
+  const int b = d.seg_begin[r], n = d.seg_len[r];  // n >= 1: a row is in its own segment
+  const uint4 qraw = *reinterpret_cast<const uint4*>(col + m * ld);
+  float qs[8], kn[8];
+  load_f8(d.q_norm + d0, qs);
+  load_f8(d.k_norm + d0, kn);
+  int jr[MAXG];
+#pragma unroll
+  for (int i = 0; i < MAXG; ++i) jr[i] = d.perm[b + min(i, n - 1)];
+  int kg[MAXG];
+  uint4 kr[MAXG], vr[MAXG];
+#pragma unroll
+  for (int i = 0; i < MAXG; ++i) {
+    const long long mk = (long long)jr[i] * p + pi;
+    kg[i] = d.grp[mk];
+    kr[i] = *reinterpret_cast<const uint4*>(col + mk * ld + E);
+    vr[i] = *reinterpret_cast<const uint4*>(col + mk * ld + 2 * E);
+  }
+  __builtin_amdgcn_sched_barrier(0);  // every member's loads issued before the first is used
+  // The segment's softmax is computed for every query (so the loads above stay
+  // where they are issued) and replaced for an all-PAD patch below.
   float o[8];
+#pragma unroll
+  for (int e = 0; e < 8; ++e) o[e] = 0.0f;
+  {
+    float qn[8];
+    unpack8(qraw, qn);
+    float ss = 0.0f;
+#pragma unroll
+    for (int e = 0; e < 8; ++e) ss += qn[e] * qn[e];
+    const float dq = sqrtf(lane_sum8(ss) / (float)HD + 1e-8f);
+#pragma unroll
+    for (int e = 0; e < 8; ++e) qn[e] = (qn[e] / dq) * qs[e];
+    float sc[MAXG];
+    float mx = -INFINITY;
+#pragma unroll
+    for (int i = 0; i < MAXG; ++i) {
+      float kx[8];
+      unpack8(kr[i], kx);
+      float ks = 0.0f, dot = 0.0f;
+#pragma unroll
+      for (int e = 0; e < 8; ++e) {
+        ks += kx[e] * kx[e];
+        dot += qn[e] * (kx[e] * kn[e]);
+      }
+      ks = lane_sum8(ks);
+      dot = lane_sum8(dot);
+      sc[i] = i < n && kg[i] == gq ? (dot / sqrtf(ks / (float)HD + 1e-8f)) * 0.125f : -INFINITY;
+      mx = fmaxf(mx, sc[i]);
+    }
+    float l = 0.0f;
+#pragma unroll
+    for (int i = 0; i < MAXG; ++i) {
+      const float pw = i < n && kg[i] == gq ? __expf(sc[i] - mx) : 0.0f;
+      float vx[8];
+      unpack8(vr[i], vx);
+      l += pw;
+#pragma unroll
+      for (int e = 0; e < 8; ++e) o[e] += pw * vx[e];
+    }
+    const float inv = 1.0f / l;  // the query's own row is in its segment with its group: l >= 1
+#pragma unroll
+    for (int e = 0; e < 8; ++e) o[e] *= inv;
+  }
   if (gq < 0) {  // all-PAD patch: every score is -1e9, uniform weights over all v rows
 #pragma unroll
     for (int e = 0; e < 8; ++e) o[e] = 0.0f;
@@ -674,70 +737,6 @@ __global__ __launch_bounds__(256) void k_group_attn_seg(const AttnDesc d) {
       for (int e = 0; e < 8; ++e) o[e] += vv[e];
     }
     const float inv = 1.0f / (float)v;
-#pragma unroll
-    for (int e = 0; e < 8; ++e) o[e] *= inv;
-  } else {
-    const int b = d.seg_begin[r], n = d.seg_len[r];
-    int jr[MAXG];
-#pragma unroll
-    for (int i = 0; i < MAXG; ++i) jr[i] = i < n ? d.perm[b + i] : 0;
-    int kg[MAXG];
-    uint4 kr[MAXG], vr[MAXG];
-#pragma unroll
-    for (int i = 0; i < MAXG; ++i) {
-      kg[i] = -2;  // gq >= 0 here, so -2 matches nothing
-      if (i < n) {
-        const long long mk = (long long)jr[i] * p + pi;
-        kg[i] = d.grp[mk];
-        kr[i] = *reinterpret_cast<const uint4*>(col + mk * ld + E);
-        vr[i] = *reinterpret_cast<const uint4*>(col + mk * ld + 2 * E);
-      }
-    }
-    float qn[8], kn[8];
-    unpack8(*reinterpret_cast<const uint4*>(col + m * ld), qn);
-#pragma unroll
-    for (int e = 0; e < 8; ++e) kn[e] = d.k_norm[d0 + e];
-    float ss = 0.0f;
-#pragma unroll
-    for (int e = 0; e < 8; ++e) ss += qn[e] * qn[e];
-    const float dq = sqrtf(lane_sum8(ss) / (float)HD + 1e-8f);
-#pragma unroll
-    for (int e = 0; e < 8; ++e) qn[e] = (qn[e] / dq) * d.q_norm[d0 + e];
-    float sc[MAXG];
-    float mx = -INFINITY;
-#pragma unroll
-    for (int i = 0; i < MAXG; ++i) {
-      sc[i] = -INFINITY;
-      if (i < n) {
-        float kx[8];
-        unpack8(kr[i], kx);
-        float ks = 0.0f, dot = 0.0f;
-#pragma unroll
-        for (int e = 0; e < 8; ++e) {
-          ks += kx[e] * kx[e];
-          dot += qn[e] * (kx[e] * kn[e]);
-        }
-        ks = lane_sum8(ks);
-        dot = lane_sum8(dot);
-        if (kg[i] == gq) sc[i] = (dot / sqrtf(ks / (float)HD + 1e-8f)) * 0.125f;
-        mx = fmaxf(mx, sc[i]);
-      }
-    }
-    float l = 0.0f;
-#pragma unroll
-    for (int e = 0; e < 8; ++e) o[e] = 0.0f;
-#pragma unroll
-    for (int i = 0; i < MAXG; ++i) {
-      if (i < n && kg[i] == gq) {
-        const float pw = __expf(sc[i] - mx);
-        float vx[8];
-        unpack8(vr[i], vx);
-        l += pw;
-#pragma unroll
-        for (int e = 0; e < 8; ++e) o[e] += pw * vx[e];
-      }
-    }
-    const float inv = 1.0f / l;  // the query's own row is in its segment with its group: l >= 1
 #pragma unroll
     for (int e = 0; e < 8; ++e) o[e] *= inv;
   }
@@ -818,7 +817,9 @@ void launch_group_attention(const AttnDesc& d, hipStream_t s) {
   if (!d.perm || !d.seg_begin || !d.seg_len) throw Error(T0H_ERR_INVALID_ARG, "group attention: null segment arrays");
   const long long lanes = (long long)d.v * d.p * d.heads * 8;
   const dim3 grid((unsigned)((lanes + 255) / 256));
-  if (d.seg_max > 4 && d.seg_max <= 8)
+  if (d.seg_max <= 4)
+    hipLaunchKernelGGL(k_group_attn_seg<4>, grid, dim3(256), 0, s, d);
+  else if (d.seg_max <= 8)
     hipLaunchKernelGGL(k_group_attn_seg<8>, grid, dim3(256), 0, s, d);
   else
     hipLaunchKernelGGL(k_group_attn, grid, dim3(256), 0, s, d);
