@@ -94,7 +94,8 @@ def median_time(fn, reps):
 def other_workloads(torch, t0hip, engine, cfg, with_cpu, reps=5):
     """BASELINE configs 3 and 5 through the host-buffer entry points (upload of the context and
     download of the result included, as the reference's own bench times them), median of `reps`
-    after one warm-up; the oracle beside each on a bounded sample when `with_cpu`."""
+    after one warm-up, and config 3 also with device-resident input and output; the oracle beside
+    each on a bounded sample when `with_cpu`."""
     res = {}
     gguf = t0hip.synth_model_gguf(cfg, quant=t0hip.Q8_0, seed=0)
     model = t0hip.load_model_from_gguf(engine, gguf)
@@ -113,7 +114,21 @@ def other_workloads(torch, t0hip, engine, cfg, with_cpu, reps=5):
     if om is not None:
         om.forecast(x3, 1, x3.size, 64)
         res["config3"]["cpu_ms_per_forecast"] = round(median_time(lambda: om.forecast(x3, 1, x3.size, 64), 3) * 1e3, 1)
-    log(f"config 3: {ms3:.3f} ms per forecast")
+    # the same forecast with the context already in HBM and the output left there
+    # (t0h_forecast_grouped_dev), ten back to back and one synchronization: device time
+    d_x3 = torch.tensor(x3, device="cuda").reshape(1, -1)
+    d_o3 = torch.empty((1, 64, cfg.n_quantiles), dtype=torch.float32, device="cuda")
+    g3 = np.zeros(1, np.int64)
+    torch.cuda.synchronize()
+
+    def dev3():
+        for _ in range(10):
+            t0hip.forecast_grouped_dev(model, d_x3.data_ptr(), g3, x3.size, 64, d_o3.data_ptr())
+        torch.cuda.synchronize()
+
+    dev3()
+    res["config3"]["device_ms_per_forecast"] = round(median_time(dev3, 2 * reps) * 1e2, 3)
+    log(f"config 3: {ms3:.3f} ms per forecast ({res['config3']['device_ms_per_forecast']:.3f} device)")
 
     x5, g5 = config5_inputs()
     t_ctx, h, steps = x5.shape[1], 64, 8
