@@ -1648,16 +1648,25 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2))) void k
 // 16 lanes per weight row, 16 rows per workgroup (SwiGLU: 8 gate rows and
 // their 8 up rows).  A lane owns whole 2-block spans of its row (68 B Q8_0 /
 // 36 B Q4_0; a row is K/64 spans, so every span is 4-byte aligned), all of
-// them loaded before the first is used.  Dequantization is exact f32: with u
-// the offset byte (q + 128) or the nibble (q + 8), fma(d, u, -128 d) and
-// fma(d, u, -8 d) are the exact product f32(d) * q (gguf.rs:116-126, 159-174).
+// them loaded before the first is used.  Arithmetic is f32 with the block scale
+// factored out (gguf.rs:116-126, 159-174): a block adds d * sum(q x) for Q8_0 (q
+// the signed byte) and d * (sum(u x) - 8 sum(x)) for Q4_0 (u = q + 8 the nibble),
+// so a value costs one byte-to-float conversion and one FMA.
 // Activations of the MT rows are staged per 1024-wide K tile in LDS as f32
 // with each 64-value span padded to 68 floats, so the 16 spans a row group
 // reads in one instruction fall in distinct banks (the four row groups of a
-// wave read the same addresses: broadcast).  f32 FMAs, then a 16-lane DPP
-// reduction and the shared output stage.
+// wave read the same addresses: broadcast); for Q4_0 the pad holds the span's
+// two block sums of x.  Then a 16-lane DPP reduction and the shared output stage.
 // ---------------------------------------------------------------------------
 constexpr int GS_NR = 16, GS_TILE = 1024, GS_XS = (GS_TILE / 64) * 68;
+// A value the optimizer cannot see into: masked nibble dwords stay whole, so each
+// byte becomes one v_cvt_f32_ubyte0..3 instead of a 4-bit field extract per value.
+__device__ __forceinline__ uint32_t opaque_u32(uint32_t x) {
+  asm("" : "+v"(x));
+  return x;
+}
+// The sum of one 32-value block of activations held as a float4 by each of 8 aligned lanes.
+__device__ __forceinline__ float block_sum8(float4 v) { return lane_sum8((v.x + v.y) + (v.z + v.w)); }
 // The medium-M kernel takes 16 < M < 1024 up to MID_MN_MAX outputs: each of its
 // 32-column workgroups reads the whole activation block, so past about 512 x
 // 2304 outputs the LDS-staged 128x128 tiles measured faster (M = 512, N = 4096:
@@ -1678,27 +1687,63 @@ __global__ __launch_bounds__(256) void k_gemv_s(const GemmDesc d) {
   // rows past N read row r0 (never stored)
   const int wrow = (rloc < valid ? r0 + rloc : r0) + (SWI && g >= 8 ? N : 0);
   const uint32_t* wr = reinterpret_cast<const uint32_t*>(d.w) + (size_t)wrow * nsp * DW;
+  // One row (MT = 1): every K tile of it is staged at once, tile t at xs + t * GS_XS,
+  // its loads issued before the weights' so that the stores wait for them alone.
+  constexpr bool ALL = MT == 1;
+  constexpr int XI = ALL ? NP * GS_TILE / 1024 : 1;  // 16-byte chunks a thread loads
+  float4 xv[XI];
+  int xk[XI];
+  if constexpr (ALL) {
+    const int n4 = K / 4;
+#pragma unroll
+    for (int it = 0; it < XI; ++it) {
+      xk[it] = min(tid + 256 * it, n4 - 1) * 4;
+      if (A32) {
+        xv[it] = *reinterpret_cast<const float4*>(static_cast<const float*>(d.a) + xk[it]);
+      } else {
+        const half4 hh = *reinterpret_cast<const half4*>(static_cast<const _Float16*>(d.a) + xk[it]);
+        xv[it] = make_float4((float)hh[0], (float)hh[1], (float)hh[2], (float)hh[3]);
+      }
+    }
+  }
+  // A span is 4-byte aligned: 16-byte loads from it (4 + 1 for Q8_0's 17 dwords, 2 + 1
+  // for Q4_0's 9) instead of one load per dword; spans past the row read its last
+  // span (no branch: a load under one is waited for inside it) and are not used.
   uint32_t w[NP][DW];
 #pragma unroll
   for (int t = 0; t < NP; ++t) {
-    const int s = t * 16 + sp;
-    if (s < nsp) {
-      const uint32_t* src = wr + s * DW;  // DW contiguous dwords
+    const uint32_t* src = wr + min(t * 16 + sp, nsp - 1) * DW;
 #pragma unroll
-      for (int i = 0; i < DW; ++i) w[t][i] = src[i];
+    for (int q = 0; q < DW / 4; ++q) {
+      const uint4 u = *reinterpret_cast<const uint4*>(src + 4 * q);
+      w[t][4 * q] = u.x, w[t][4 * q + 1] = u.y, w[t][4 * q + 2] = u.z, w[t][4 * q + 3] = u.w;
     }
+    w[t][DW - 1] = src[DW - 1];
   }
   float acc[MT];
 #pragma unroll
   for (int m = 0; m < MT; ++m) acc[m] = 0.0f;
 
+  if constexpr (ALL) {
+    // (past the row: the last chunk again, written to its own place: the same value)
+#pragma unroll
+    for (int it = 0; it < XI; ++it) {
+      const int k4 = xk[it], t = k4 / GS_TILE, kk = k4 % GS_TILE;
+      *reinterpret_cast<float4*>(xs + t * GS_XS + (kk >> 6) * 68 + (kk & 63)) = xv[it];
+      if constexpr (WT == T0H_Q4_0) {
+        const float bsum = block_sum8(xv[it]);
+        if ((tid & 7) == 0 && tid + 256 * it < K / 4) xs[t * GS_XS + (kk >> 6) * 68 + 64 + ((kk >> 5) & 1)] = bsum;
+      }
+    }
+    __syncthreads();
+  }
 #pragma unroll
   for (int t = 0; t < NP; ++t) {
     const int k0 = t * GS_TILE;
     if (k0 >= K) break;
     const int kn = min(GS_TILE, K - k0);
-    if (t) __syncthreads();  // the previous tile is consumed
-    for (int i = tid; i < MT * (kn / 4); i += 256) {
+    if (!ALL && t) __syncthreads();  // the previous tile is consumed
+    for (int i = tid; !ALL && i < MT * (kn / 4); i += 256) {
       const int m = i / (kn / 4), k4 = (i % (kn / 4)) * 4;
       float4 v = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
       if (m < M) {
@@ -1710,44 +1755,57 @@ __global__ __launch_bounds__(256) void k_gemv_s(const GemmDesc d) {
         }
       }
       *reinterpret_cast<float4*>(xs + m * GS_XS + (k4 >> 6) * 68 + (k4 & 63)) = v;
+      if constexpr (WT == T0H_Q4_0) {
+        const float bsum = block_sum8(v);
+        if ((tid & 7) == 0) xs[m * GS_XS + (k4 >> 6) * 68 + 64 + ((k4 >> 5) & 1)] = bsum;
+      }
     }
-    __syncthreads();
+    if (!ALL) __syncthreads();
     const int s = t * 16 + sp;
     if (s < nsp) {
       const uint32_t* r = w[t];
-      const float* xr = xs + sp * 68;
+      const float* xr = xs + (ALL ? t * GS_XS : 0) + sp * 68;
 #pragma unroll
       for (int h = 0; h < 2; ++h) {
         // block h of the span: d at byte (DW*2)*h, quants after it
         const int bo = h * (DW * 2);  // byte offset of the block (34 or 18 per block)
         const uint32_t dw = r[bo >> 2];
         const float dv = (float)__builtin_bit_cast(_Float16, (uint16_t)((bo & 3) ? (dw >> 16) : (dw & 0xffff)));
-        const float nofs = (WT == T0H_Q8_0 ? -128.0f : -8.0f) * dv;
+        float bs[MT];
+#pragma unroll
+        for (int m = 0; m < MT; ++m) bs[m] = 0.0f;
 #pragma unroll
         for (int pc = 0; pc < 4; ++pc) {  // 8 consecutive values k = 32h + 8pc .. +7
           float wv[8];
 #pragma unroll
           for (int e = 0; e < 8; ++e) {
-            uint32_t u;
             if (WT == T0H_Q8_0) {
               const int b = bo + 2 + pc * 8 + e;  // byte of value 8pc + e
-              u = ((r[b >> 2] >> (8 * (b & 3))) & 0xffu) ^ 0x80u;
+              wv[e] = (float)(int8_t)(r[b >> 2] >> (8 * (b & 3)));
             } else {
-              const int j = (pc & 1) * 8 + e;  // quant byte; high nibbles for values >= 16
-              const int b = bo + 2 + j;
-              u = (r[b >> 2] >> (8 * (b & 3) + (pc >= 2 ? 4 : 0))) & 0xfu;
+              // quant byte j; high nibbles for values >= 16; the nibbles of a whole
+              // dword are masked at once, then each byte converted on its own
+              const int j = (pc & 1) * 8 + e, b = bo + 2 + j;
+              const uint32_t q = r[b >> 2], nib = opaque_u32((pc >= 2 ? q >> 4 : q) & 0x0f0f0f0fu);
+              wv[e] = (float)((nib >> (8 * (b & 3))) & 0xffu);
             }
-            wv[e] = fmaf(dv, (float)u, nofs);
           }
 #pragma unroll
           for (int m = 0; m < MT; ++m) {
             const float4 xa = *reinterpret_cast<const float4*>(xr + m * GS_XS + 32 * h + 8 * pc);
             const float4 xb = *reinterpret_cast<const float4*>(xr + m * GS_XS + 32 * h + 8 * pc + 4);
-            float a = acc[m];
+            float a = bs[m];
             a = fmaf(wv[0], xa.x, a); a = fmaf(wv[1], xa.y, a); a = fmaf(wv[2], xa.z, a); a = fmaf(wv[3], xa.w, a);
             a = fmaf(wv[4], xb.x, a); a = fmaf(wv[5], xb.y, a); a = fmaf(wv[6], xb.z, a); a = fmaf(wv[7], xb.w, a);
-            acc[m] = a;
+            bs[m] = a;
           }
+        }
+#pragma unroll
+        for (int m = 0; m < MT; ++m) {
+          if (WT == T0H_Q8_0)
+            acc[m] = fmaf(dv, bs[m], acc[m]);
+          else
+            acc[m] = fmaf(dv, fmaf(-8.0f, xr[m * GS_XS + 64 + h], bs[m]), acc[m]);
         }
       }
     }
@@ -1762,6 +1820,140 @@ __global__ __launch_bounds__(256) void k_gemv_s(const GemmDesc d) {
   }
   __syncthreads();
   gemv_store<EPI, MT, GS_NR>(d, fin, tid, r0, valid, 0);
+}
+
+// ---------------------------------------------------------------------------
+// M = 1 kernel for long Q8_0 / Q4_0 rows: K = 4096 SP (SP = 1, 2), 64 SP
+// two-block spans a row.  Lane l of a wave owns spans l + 64 j of every row the
+// wave takes, so the activations of those spans are read from LDS into its
+// registers once and serve all of its rows: a row then costs one coalesced load
+// of 64 x 36 (Q4_0) or 68 (Q8_0) bytes a span column and, a value, one
+// byte-to-float conversion and one FMA, with the block scale factored out as in
+// k_gemv_s.  Q4_0 nibbles: the low ones masked to bytes (u), the high ones kept
+// in place (16 u, an exact power-of-two scale undone once a block).  A wave
+// takes R rows, all loaded before the first is used; the four waves' row
+// partials meet in LDS and 8 lanes finish each row.
+// ---------------------------------------------------------------------------
+// Rows a wave takes: 4 (16 a workgroup, so K = 4096, N = 16384 fills 1024 workgroups),
+// 2 when the activations take 128 registers (K = 8192).
+constexpr int gw_rows(int sp) { return sp == 1 ? 4 : 2; }
+
+template <int WT, bool A32, int EPI, int SP>
+__global__ __launch_bounds__(256) void k_gemv_w(const GemmDesc d) {
+  extern __shared__ __align__(16) float xs[];  // 64 SP spans of 68 floats, then the row partials
+  constexpr int DW = WT == T0H_Q8_0 ? 17 : 9;  // dwords per span
+  constexpr int R = gw_rows(SP), NRW = 4 * R;
+  constexpr bool SWI = EPI == EPI_SWIGLU_F16;
+  constexpr int PER = SWI ? NRW / 2 : NRW;  // output columns of a workgroup
+  constexpr int XI = SP * 4;                // 16-byte activation chunks a thread stages
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int N = d.N, nsp = 64 * SP;
+  const int r0 = blockIdx.x * PER;
+  const int valid = min(PER, N - r0);
+  float4 xv[XI];
+#pragma unroll
+  for (int it = 0; it < XI; ++it) {
+    const int k = (tid + 256 * it) * 4;
+    if (A32) {
+      xv[it] = *reinterpret_cast<const float4*>(static_cast<const float*>(d.a) + k);
+    } else {
+      const half4 hh = *reinterpret_cast<const half4*>(static_cast<const _Float16*>(d.a) + k);
+      xv[it] = make_float4((float)hh[0], (float)hh[1], (float)hh[2], (float)hh[3]);
+    }
+  }
+  // local row w R + i: output column c (SwiGLU: gate rows, then their up rows);
+  // columns past N read the workgroup's first row (never stored)
+  uint32_t w[R][SP][DW];
+#pragma unroll
+  for (int i = 0; i < R; ++i) {
+    const int lr = wave * R + i, c = SWI && lr >= PER ? lr - PER : lr;
+    const int row = (c < valid ? r0 + c : r0) + (SWI && lr >= PER ? N : 0);
+    const uint32_t* wr = reinterpret_cast<const uint32_t*>(d.w) + (size_t)row * nsp * DW;
+#pragma unroll
+    for (int j = 0; j < SP; ++j) {
+      const uint32_t* src = wr + (lane + 64 * j) * DW;
+#pragma unroll
+      for (int q = 0; q < DW / 4; ++q) {
+        const uint4 u = *reinterpret_cast<const uint4*>(src + 4 * q);
+        w[i][j][4 * q] = u.x, w[i][j][4 * q + 1] = u.y, w[i][j][4 * q + 2] = u.z, w[i][j][4 * q + 3] = u.w;
+      }
+      w[i][j][DW - 1] = src[DW - 1];
+    }
+  }
+#pragma unroll
+  for (int it = 0; it < XI; ++it) {
+    const int k = (tid + 256 * it) * 4;
+    *reinterpret_cast<float4*>(xs + (k >> 6) * 68 + (k & 63)) = xv[it];
+  }
+  __syncthreads();
+  float x[SP][64];
+#pragma unroll
+  for (int j = 0; j < SP; ++j) {
+#pragma unroll
+    for (int c = 0; c < 16; ++c) {
+      const float4 v = *reinterpret_cast<const float4*>(xs + (lane + 64 * j) * 68 + 4 * c);
+      x[j][4 * c] = v.x, x[j][4 * c + 1] = v.y, x[j][4 * c + 2] = v.z, x[j][4 * c + 3] = v.w;
+    }
+  }
+  float sx[SP][2];  // Q4_0: the block sums of x
+#pragma unroll
+  for (int j = 0; j < SP; ++j) {
+#pragma unroll
+    for (int h = 0; h < 2; ++h) {
+      float a = 0.0f;
+#pragma unroll
+      for (int v = 0; v < 32; ++v) a += x[j][32 * h + v];
+      sx[j][h] = WT == T0H_Q4_0 ? a : 0.0f;
+    }
+  }
+  float* part = xs + 64 * SP * 68;
+#pragma unroll
+  for (int i = 0; i < R; ++i) {
+    float acc = 0.0f;
+#pragma unroll
+    for (int j = 0; j < SP; ++j) {
+      const uint32_t* r = w[i][j];
+#pragma unroll
+      for (int h = 0; h < 2; ++h) {
+        const int bo = h * (DW * 2);  // byte offset of block h (34 or 18 bytes a block)
+        const uint32_t dw = r[bo >> 2];
+        const float dv = (float)__builtin_bit_cast(_Float16, (uint16_t)((bo & 3) ? (dw >> 16) : (dw & 0xffff)));
+        if (WT == T0H_Q8_0) {
+          float b0 = 0.0f, b1 = 0.0f;
+#pragma unroll
+          for (int v = 0; v < 32; v += 2) {
+            const int b = bo + 2 + v, c = b + 1;
+            b0 = fmaf((float)(int8_t)(r[b >> 2] >> (8 * (b & 3))), x[j][32 * h + v], b0);
+            b1 = fmaf((float)(int8_t)(r[c >> 2] >> (8 * (c & 3))), x[j][32 * h + v + 1], b1);
+          }
+          acc = fmaf(dv, b0 + b1, acc);
+        } else {
+          float bl = 0.0f, bh = 0.0f;  // low nibbles (values 0..15), high nibbles x 16 (16..31)
+#pragma unroll
+          for (int v = 0; v < 16; ++v) {
+            const int b = bo + 2 + v;
+            const uint32_t lo = opaque_u32(r[b >> 2] & 0x0f0f0f0fu), hi = opaque_u32(r[b >> 2] & 0xf0f0f0f0u);
+            bl = fmaf((float)((lo >> (8 * (b & 3))) & 0xffu), x[j][32 * h + v], bl);
+            bh = fmaf((float)((hi >> (8 * (b & 3))) & 0xffu), x[j][32 * h + 16 + v], bh);
+          }
+          acc = fmaf(dv, fmaf(-8.0f, sx[j][h], fmaf(bh, 0.0625f, bl)), acc);
+        }
+      }
+    }
+    part[(wave * R + i) * 64 + lane] = acc;
+  }
+  __syncthreads();
+  // row t / 8 summed by 8 lanes (aligned groups: all active); the activations are
+  // no longer read, so the row sums reuse their LDS
+  float rsum = 0.0f;
+  if (tid < NRW * 8) {
+    const float4 a = *reinterpret_cast<const float4*>(part + tid * 8);
+    const float4 b = *reinterpret_cast<const float4*>(part + tid * 8 + 4);
+    rsum = lane_sum8(((a.x + a.y) + (a.z + a.w)) + ((b.x + b.y) + (b.z + b.w)));
+  }
+  if (tid < NRW * 8 && (tid & 7) == 0) xs[tid >> 3] = rsum;
+  __syncthreads();
+  gemv_store<EPI, 1, NRW>(d, xs, tid, r0, valid, 0);
 }
 
 // ---------------------------------------------------------------------------
@@ -2068,12 +2260,24 @@ void run_gemv(const GemmDesc& d, hipStream_t s) {
 template <int WT, bool A32, int EPI, int MT, int NP>
 void run_gemv_s(const GemmDesc& d, hipStream_t s) {
   if (d.row_ssq || d.norm_out) throw Error(T0H_ERR_HIP, "internal: split RMSNorm on a kernel without it");
-  const size_t lds = (size_t)MT * GS_XS * sizeof(float);
+  const size_t lds = (size_t)(MT == 1 ? NP : MT) * GS_XS * sizeof(float);
   const int per = EPI == EPI_SWIGLU_F16 ? GS_NR / 2 : GS_NR;
   static std::atomic<uint64_t> lds_set{0};  // per instantiation
   allow_dynamic_lds(reinterpret_cast<const void*>(&k_gemv_s<WT, A32, EPI, MT, NP>), lds_set);
   hipLaunchKernelGGL((k_gemv_s<WT, A32, EPI, MT, NP>), dim3((d.N + per - 1) / per), dim3(256), lds, s, d);
   check_hip(hipGetLastError(), "k_gemv_s launch");
+}
+
+template <int WT, bool A32, int EPI, int SP>
+void run_gemv_w(const GemmDesc& d, hipStream_t s) {
+  if (d.row_ssq || d.norm_out) throw Error(T0H_ERR_HIP, "internal: split RMSNorm on a kernel without it");
+  if (d.M != 1 || d.K != 4096 * SP) throw Error(T0H_ERR_HIP, "internal: gemv_w shape");
+  constexpr int NRW = 4 * gw_rows(SP), per = EPI == EPI_SWIGLU_F16 ? NRW / 2 : NRW;
+  const size_t lds = (size_t)(64 * SP * 68 + NRW * 64) * sizeof(float);
+  static std::atomic<uint64_t> lds_set{0};  // per instantiation
+  allow_dynamic_lds(reinterpret_cast<const void*>(&k_gemv_w<WT, A32, EPI, SP>), lds_set);
+  hipLaunchKernelGGL((k_gemv_w<WT, A32, EPI, SP>), dim3((d.N + per - 1) / per), dim3(256), lds, s, d);
+  check_hip(hipGetLastError(), "k_gemv_w launch");
 }
 
 template <int WT, bool A32, int EPI, int MT>
@@ -2092,6 +2296,8 @@ void dispatch_gemv(const GemmDesc& d, hipStream_t s) {
   // every activation row per weight row: M = 16 took 10 us at K = 768, N = 2304)
   if (gemv_mf_ok(d)) return run_gemv_mf<WT, A32, EPI>(d, s);
   if constexpr (WT != T0H_F16) {
+    if (d.M == 1 && d.K == 4096) return run_gemv_w<WT, A32, EPI, 1>(d, s);
+    if (d.M == 1 && d.K == 8192) return run_gemv_w<WT, A32, EPI, 2>(d, s);
     if (d.M <= 16 && d.K % 64 == 0 && d.K <= 4 * GS_TILE) {
       if (d.M == 1) return dispatch_gemv_s<WT, A32, EPI, 1>(d, s);
       if (d.M <= 4) return dispatch_gemv_s<WT, A32, EPI, 4>(d, s);

@@ -237,6 +237,22 @@ def test_small_m_kernel(torch_cuda, t0hip, oracle, rng, qtype, m, k, n):
     assert rel_err(got, np.maximum(want, 0.0)) < 1e-5, (m, k, n)
 
 
+@pytest.mark.parametrize("qtype", [8, 2])
+@pytest.mark.parametrize("k,n", [(4096, 200), (4096, 4104), (8192, 72), (8192, 1031)])
+def test_gemv_long_rows(torch_cuda, t0hip, oracle, rng, qtype, k, n):
+    """M = 1 at K = 4096 and 8192 through t0h_gemm_q (the kernel that holds a lane's activation
+    spans in registers across its weight rows): exact f32, so the 1e-5 gate of the reference's
+    f32 kernels holds, with and without ReLU; N not a multiple of a workgroup's rows."""
+    W = (0.02 * rng.standard_normal((n, k))).astype(np.float32)
+    x = rng.standard_normal((1, k)).astype(np.float32)
+    b = (0.02 * rng.standard_normal(n)).astype(np.float32)
+    blocks = oracle.quantize(qtype, W)
+    deq = oracle.dequantize(qtype, blocks, n * k).reshape(n, k).astype(np.float64)
+    want = x.astype(np.float64) @ deq.T + b
+    assert rel_err(run_gemm(torch_cuda, t0hip, qtype, blocks, x, b, n), want) < 1e-5, (k, n)
+    assert rel_err(run_gemm(torch_cuda, t0hip, qtype, blocks, x, b, n, act=1), np.maximum(want, 0.0)) < 1e-5
+
+
 @pytest.mark.parametrize("qtype", [8, 2, 1])
 @pytest.mark.parametrize("m,k,n", [(2, 96, 40), (3, 160, 33), (5, 4096, 300), (16, 32, 17), (12, 1056, 24),
                                    (16, 4096, 2048)])
@@ -256,7 +272,8 @@ def test_small_m_f32_mfma_kernel(torch_cuda, t0hip, oracle, rng, qtype, m, k, n)
 
 @pytest.mark.parametrize("qtype", [8, 2, 1])
 @pytest.mark.parametrize("epi", [0, 1, 2, 3])
-@pytest.mark.parametrize("m,k,n", [(1, 768, 136), (9, 2048, 72), (16, 768, 40), (2, 96, 24)])
+@pytest.mark.parametrize("m,k,n", [(1, 768, 136), (1, 4096, 136), (1, 8192, 40), (9, 2048, 72), (16, 768, 40),
+                                   (2, 96, 24)])
 def test_small_m_forward_epilogues(torch_cuda, t0hip, oracle, rng, qtype, epi, m, k, n):
     """The forward's GEMMs at M <= 16 (a single series, the decoder's forecast rows): f16
     activations, epilogues bias / f16 store / residual add / SwiGLU on the small-M kernels
