@@ -174,6 +174,37 @@ def gemm_bytes(name, M, cfg, wbytes_per_val):
     return None
 
 
+def stream_read_us(torch, buf, nbytes, n_copies, reps):
+    """Event-timed average of t0p_stream_read over nbytes of each of the n_copies copies in buf
+    (libt0probe.so, a measurement helper built beside libt0hip.so); None when it is not built."""
+    import ctypes
+
+    path = os.path.join(ROOT, "t0-web_amd", "libt0probe.so")
+    if not os.path.exists(path):
+        return None
+    lib = ctypes.CDLL(path)
+    lib.t0p_stream_read.argtypes = [ctypes.c_void_p, ctypes.c_size_t, ctypes.c_void_p, ctypes.c_void_p]
+    lib.t0p_stream_read_out_words.argtypes = [ctypes.c_size_t]
+    lib.t0p_stream_read_out_words.restype = ctypes.c_size_t
+    out = torch.empty(int(lib.t0p_stream_read_out_words(nbytes)), dtype=torch.int32, device="cuda")
+    stream = torch.cuda.current_stream()
+
+    def run(i):
+        rc = lib.t0p_stream_read(buf.data_ptr() + (i % n_copies) * nbytes, nbytes, out.data_ptr(), stream.cuda_stream)
+        if rc != 0:
+            raise RuntimeError(f"t0p_stream_read: hip error {rc}")
+
+    for i in range(3):
+        run(i)
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e0.record(stream)
+    for i in range(reps):
+        run(i)
+    e1.record(stream)
+    torch.cuda.synchronize()
+    return e0.elapsed_time(e1) * 1e3 / reps
+
+
 def gemm_sweep(torch, t0hip, iters=20):
     """BASELINE configs 1-2 through the kernel-level t0h_gemm_q (f32 x in, f32 y out)."""
     rng = np.random.default_rng(7)
@@ -215,8 +246,16 @@ def gemm_sweep(torch, t0hip, iters=20):
                 ai = flops / nbytes
                 bound = "mfma" if ai * HBM_PEAK_GBS * 1e9 > MFMA_F16_PEAK_TFLOPS * 1e12 else "hbm"
                 frac = tflops / MFMA_F16_PEAK_TFLOPS if bound == "mfma" else gbs / HBM_PEAK_GBS
-                out.append({"quant": qname, "M": M, "K": K, "N": N, "us": round(us, 2), "tflops": round(tflops, 2),
-                            "gbs": round(gbs, 1), "bound": bound, "frac": round(frac, 3)})
+                rec = {"quant": qname, "M": M, "K": K, "N": N, "us": round(us, 2), "tflops": round(tflops, 2),
+                       "gbs": round(gbs, 1), "bound": bound, "frac": round(frac, 3)}
+                if M == 1 and N * K > 2**24:
+                    # the same weight copies read once by a plain streaming-read kernel, timed the same way:
+                    # what a launch that only reads these bytes costs on this box
+                    rd_us = stream_read_us(torch, dW, stride, n_copies, reps)
+                    if rd_us is not None:
+                        rec["read_only_us"] = round(rd_us, 2)
+                        rec["read_only_frac"] = round(stride / rd_us * 1e-3 / HBM_PEAK_GBS, 3)
+                out.append(rec)
                 del dW, x, y
     return out
 

@@ -26,6 +26,24 @@ def test_every_declared_symbol_is_exported(t0hip):
     assert sorted(t0hip.SYMBOLS) == names
 
 
+def test_probe_library_is_separate(t0hip):
+    """The benchmark's streaming-read helper lives in its own library, outside the C ABI: it
+    exports its two entry points, rejects bad sizes before touching a device, and
+    libt0hip.so exports none of them."""
+    path = os.path.join(ROOT, "t0-web_amd", "libt0probe.so")
+    if not os.path.exists(path):
+        pytest.skip("libt0probe.so not built")
+    P = C.CDLL(path)
+    P.t0p_stream_read.argtypes = [C.c_void_p, C.c_size_t, C.c_void_p, C.c_void_p]
+    P.t0p_stream_read_out_words.argtypes = [C.c_size_t]
+    P.t0p_stream_read_out_words.restype = C.c_size_t
+    assert P.t0p_stream_read_out_words(65536) == 1 and P.t0p_stream_read_out_words(65552) == 2
+    assert P.t0p_stream_read(None, 64, None, None) != 0
+    assert P.t0p_stream_read(C.c_void_p(16), 24, C.c_void_p(16), None) != 0  # not a multiple of 16
+    L = C.CDLL(t0hip.LIB_PATH)
+    assert not hasattr(L, "t0p_stream_read")
+
+
 def test_abi_version_and_no_device(t0hip):
     assert t0hip.lib().t0h_abi_version() == 1
     import torch
