@@ -2076,8 +2076,8 @@ void run_gemm_tiled(const GemmDesc& d, int tile, hipStream_t s) {
 
 // ---------------------------------------------------------------------------
 // Small-M kernel for 2 <= M <= 16 rows (any weight type, K % 32 == 0): exact
-// f32 products on v_mfma_f32_16x16x4f32.  A workgroup owns 16 weight rows
-// (SwiGLU: 8 gate rows and their 8 up rows) and splits K over MF_WAVES waves,
+// f32 products on v_mfma_f32_16x16x4f32.  A workgroup owns NB groups of 16 weight
+// rows (SwiGLU: 8 gate rows and their 8 up rows) and splits K over MF_WAVES waves,
 // block kb going to wave kb % MF_WAVES.  In a 32-value block, lane (j, c) =
 // (lane % 16, lane / 16) dequantizes values 8c .. 8c+7 of weight row j exactly
 // (f32(d) * q: an 11-bit scale times an integer of at most 8 bits; f16 weights
@@ -2088,44 +2088,55 @@ void run_gemm_tiled(const GemmDesc& d, int tile, hipStream_t s) {
 // The weights are read with 2-byte loads (Q8_0 / Q4_0 blocks are 2-byte
 // aligned), never past a block.
 // ---------------------------------------------------------------------------
-constexpr int MF_WAVES = 8, MF_CH = 4;  // waves per workgroup, blocks per load batch
+constexpr int MF_WAVES = 8;  // waves per workgroup
 
-template <int WT, bool A32, int EPI>
+// NB groups of 16 weight columns a workgroup (4 for wide matrices: every activation value a lane
+// loads then feeds 4 groups' MFMAs instead of one); CH blocks per load batch.
+template <int WT, bool A32, int EPI, int NB>
 __global__ __launch_bounds__(64 * MF_WAVES) void k_gemv_mf(const GemmDesc d) {
-  __shared__ float red[MF_WAVES][16][17];
+  constexpr int CH = NB == 1 ? 4 : 2;
+  __shared__ float red[NB][MF_WAVES][16][17];
   constexpr bool SWI = EPI == EPI_SWIGLU_F16;
+  constexpr int GC = SWI ? 8 : 16;  // output columns of a group
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6, j = lane & 15, c = lane >> 4;
   const int M = d.M, N = d.N, K = d.K, KB = K / 32;
-  const int c0 = blockIdx.x * (SWI ? 8 : 16);  // first output column (SwiGLU: hidden unit)
-  int wrow;
-  if (SWI) {
-    const int u = min(c0 + (j & 7), N - 1);
-    wrow = j < 8 ? u : N + u;
-  } else {
-    wrow = min(c0 + j, N - 1);  // rows past N are computed, never stored
-  }
+  const int c0 = blockIdx.x * GC * NB;  // first output column (SwiGLU: hidden unit)
   const size_t rowb = WT == T0H_F16 ? (size_t)K * 2 : (size_t)KB * block_bytes(WT);
-  const uint8_t* wr = static_cast<const uint8_t*>(d.w) + (size_t)wrow * rowb;
+  const uint8_t* wr[NB];
+#pragma unroll
+  for (int nb = 0; nb < NB; ++nb) {
+    int wrow;
+    if (SWI) {
+      const int u = min(c0 + nb * GC + (j & 7), N - 1);
+      wrow = j < 8 ? u : N + u;
+    } else {
+      wrow = min(c0 + nb * GC + j, N - 1);  // rows past N are computed, never stored
+    }
+    wr[nb] = static_cast<const uint8_t*>(d.w) + (size_t)wrow * rowb;
+  }
   const bool arow = j < M;
   const size_t aoff = (size_t)(arow ? j : 0) * d.lda + 8 * c;
 
-  // one block's operands for this lane: 8 weights (raw) and 8 activations
+  // one block's operands for this lane: 8 weights (raw) of each group and 8 activations
   struct Op {
-    uint32_t w[4];  // Q8_0 / Q4_0: 4 x 2 bytes (+ the scale in sc); f16: 8 halves
-    uint32_t sc;
+    uint32_t w[NB][4];  // Q8_0 / Q4_0: 4 x 2 bytes (+ the scale in sc); f16: 8 halves
+    uint32_t sc[NB];
     uint32_t a[A32 ? 8 : 4];
   };
   auto load = [&](int kb, Op& o) {
-    if constexpr (WT == T0H_F16) {
-      const uint4 v = *reinterpret_cast<const uint4*>(wr + (size_t)(kb * 32 + 8 * c) * 2);
-      o.w[0] = v.x, o.w[1] = v.y, o.w[2] = v.z, o.w[3] = v.w;
-      o.sc = 0;
-    } else {
-      const uint8_t* b = wr + (size_t)kb * block_bytes(WT);
-      const uint16_t* q = reinterpret_cast<const uint16_t*>(b + 2 + (WT == T0H_Q8_0 ? 8 * c : 8 * (c & 1)));
 #pragma unroll
-      for (int e = 0; e < 4; ++e) o.w[e] = q[e];
-      o.sc = *reinterpret_cast<const uint16_t*>(b);
+    for (int nb = 0; nb < NB; ++nb) {
+      if constexpr (WT == T0H_F16) {
+        const uint4 v = *reinterpret_cast<const uint4*>(wr[nb] + (size_t)(kb * 32 + 8 * c) * 2);
+        o.w[nb][0] = v.x, o.w[nb][1] = v.y, o.w[nb][2] = v.z, o.w[nb][3] = v.w;
+        o.sc[nb] = 0;
+      } else {
+        const uint8_t* b = wr[nb] + (size_t)kb * block_bytes(WT);
+        const uint16_t* q = reinterpret_cast<const uint16_t*>(b + 2 + (WT == T0H_Q8_0 ? 8 * c : 8 * (c & 1)));
+#pragma unroll
+        for (int e = 0; e < 4; ++e) o.w[nb][e] = q[e];
+        o.sc[nb] = *reinterpret_cast<const uint16_t*>(b);
+      }
     }
     if (arow) {
       if constexpr (A32) {
@@ -2143,12 +2154,12 @@ __global__ __launch_bounds__(64 * MF_WAVES) void k_gemv_mf(const GemmDesc d) {
       for (int e = 0; e < (A32 ? 8 : 4); ++e) o.a[e] = 0;
     }
   };
-  auto weight = [&](const Op& o, int s) -> float {
+  auto weight = [&](const Op& o, int nb, int s) -> float {
     if constexpr (WT == T0H_F16) {
-      return (float)__builtin_bit_cast(half2v, o.w[s >> 1])[s & 1];
+      return (float)__builtin_bit_cast(half2v, o.w[nb][s >> 1])[s & 1];
     } else {
-      const float dd = (float)__builtin_bit_cast(_Float16, (uint16_t)o.sc);
-      const uint32_t byte = (o.w[s >> 1] >> (8 * (s & 1))) & 0xffu;
+      const float dd = (float)__builtin_bit_cast(_Float16, (uint16_t)o.sc[nb]);
+      const uint32_t byte = (o.w[nb][s >> 1] >> (8 * (s & 1))) & 0xffu;
       if constexpr (WT == T0H_Q8_0) return dd * (float)(int8_t)byte;
       const uint32_t nib = c >= 2 ? byte >> 4 : byte & 15u;
       return dd * (float)((int)nib - 8);
@@ -2159,36 +2170,46 @@ __global__ __launch_bounds__(64 * MF_WAVES) void k_gemv_mf(const GemmDesc d) {
     return (float)__builtin_bit_cast(half2v, o.a[s >> 1])[s & 1];
   };
 
-  floatx4 acc = {0.0f, 0.0f, 0.0f, 0.0f};
-  // batches of MF_CH blocks, the next batch's loads issued before this one's MFMAs
-  Op ops[2][MF_CH];
-  auto load_batch = [&](int kb0, Op(&o)[MF_CH]) {
+  floatx4 acc[NB];
 #pragma unroll
-    for (int q = 0; q < MF_CH; ++q)
+  for (int nb = 0; nb < NB; ++nb) acc[nb] = floatx4{0.0f, 0.0f, 0.0f, 0.0f};
+  // batches of CH blocks, the next batch's loads issued before this one's MFMAs
+  Op ops[2][CH];
+  auto load_batch = [&](int kb0, Op(&o)[CH]) {
+#pragma unroll
+    for (int q = 0; q < CH; ++q)
       if (kb0 + q * MF_WAVES < KB) load(kb0 + q * MF_WAVES, o[q]);
   };
-  auto run_batch = [&](int kb0, const Op(&o)[MF_CH]) {
+  auto run_batch = [&](int kb0, const Op(&o)[CH]) {
 #pragma unroll
-    for (int q = 0; q < MF_CH; ++q)
+    for (int q = 0; q < CH; ++q)
       if (kb0 + q * MF_WAVES < KB) {
 #pragma unroll
-        for (int s = 0; s < 8; ++s)
-          acc = __builtin_amdgcn_mfma_f32_16x16x4f32(act(o[q], s), weight(o[q], s), acc, 0, 0, 0);
+        for (int s = 0; s < 8; ++s) {
+          const float av = act(o[q], s);
+#pragma unroll
+          for (int nb = 0; nb < NB; ++nb)
+            acc[nb] = __builtin_amdgcn_mfma_f32_16x16x4f32(av, weight(o[q], nb, s), acc[nb], 0, 0, 0);
+        }
       }
   };
-  constexpr int STEP = MF_WAVES * MF_CH;
+  constexpr int STEP = MF_WAVES * CH;
   load_batch(wave, ops[0]);
   // the output threads' bias (and old residual value), loaded with the first batch
   const int m = tid >> 4, jj = tid & 15;
-  const int col = c0 + jj;
-  const bool outp = tid < 256 && m < M && (SWI ? jj < 8 : true) && col < N;
-  float pb = 0.0f, pb2 = 0.0f, py = 0.0f;
-  if (outp) {
-    if (d.bias) {
-      pb = d.bias[col];
-      if constexpr (SWI) pb2 = d.bias[N + col];
+  float pb[NB], pb2[NB], py[NB];
+#pragma unroll
+  for (int nb = 0; nb < NB; ++nb) {
+    const int col = c0 + nb * GC + jj;
+    const bool outp = tid < 256 && m < M && (SWI ? jj < 8 : true) && col < N;
+    pb[nb] = 0.0f, pb2[nb] = 0.0f, py[nb] = 0.0f;
+    if (outp) {
+      if (d.bias) {
+        pb[nb] = d.bias[col];
+        if constexpr (SWI) pb2[nb] = d.bias[N + col];
+      }
+      if constexpr (EPI == EPI_RESID_F32) py[nb] = static_cast<const float*>(d.y)[(size_t)m * d.ldy + col];
     }
-    if constexpr (EPI == EPI_RESID_F32) py = static_cast<const float*>(d.y)[(size_t)m * d.ldy + col];
   }
   int kb0 = wave;
   for (; kb0 + STEP < KB; kb0 += 2 * STEP) {  // pairs of batches: the buffers alternate
@@ -2200,38 +2221,56 @@ __global__ __launch_bounds__(64 * MF_WAVES) void k_gemv_mf(const GemmDesc d) {
   if (kb0 < KB) run_batch(kb0, ops[0]);
   // D layout: lane l, register r -> row 4 (l / 16) + r, column l % 16
 #pragma unroll
-  for (int r = 0; r < 4; ++r) red[wave][4 * c + r][j] = acc[r];
+  for (int nb = 0; nb < NB; ++nb) {
+#pragma unroll
+    for (int r = 0; r < 4; ++r) red[nb][wave][4 * c + r][j] = acc[nb][r];
+  }
   __syncthreads();
-  if (!outp) return;
-  float v = 0.0f;
+  if (tid >= 256 || m >= M || (SWI && jj >= 8)) return;
 #pragma unroll
-  for (int w = 0; w < MF_WAVES; ++w) v += red[w][m][jj];
-  if constexpr (SWI) {
-    float up = 0.0f;
+  for (int nb = 0; nb < NB; ++nb) {
+    const int col = c0 + nb * GC + jj;
+    if (col >= N) break;
+    float v = 0.0f;
 #pragma unroll
-    for (int w = 0; w < MF_WAVES; ++w) up += red[w][m][jj + 8];
-    const float g = v + pb, uu = up + pb2;
-    static_cast<_Float16*>(d.y)[(size_t)m * d.ldy + col] = (_Float16)(silu(g) * uu);
-  } else {
-    v += pb;
-    if (d.relu) v = fmaxf(v, 0.0f);
-    const size_t o = (size_t)m * d.ldy + col;
-    if constexpr (EPI == EPI_RESID_F32) {
-      static_cast<float*>(d.y)[o] = py + v;
-    } else if constexpr (EPI == EPI_STORE_F32) {
-      static_cast<float*>(d.y)[o] = v;
+    for (int w = 0; w < MF_WAVES; ++w) v += red[nb][w][m][jj];
+    if constexpr (SWI) {
+      float up = 0.0f;
+#pragma unroll
+      for (int w = 0; w < MF_WAVES; ++w) up += red[nb][w][m][jj + 8];
+      const float g = v + pb[nb], uu = up + pb2[nb];
+      static_cast<_Float16*>(d.y)[(size_t)m * d.ldy + col] = (_Float16)(silu(g) * uu);
     } else {
-      static_cast<_Float16*>(d.y)[o] = (_Float16)v;
+      v += pb[nb];
+      if (d.relu) v = fmaxf(v, 0.0f);
+      const size_t o = (size_t)m * d.ldy + col;
+      if constexpr (EPI == EPI_RESID_F32) {
+        static_cast<float*>(d.y)[o] = py[nb] + v;
+      } else if constexpr (EPI == EPI_STORE_F32) {
+        static_cast<float*>(d.y)[o] = v;
+      } else {
+        static_cast<_Float16*>(d.y)[o] = (_Float16)v;
+      }
     }
   }
 }
 
+template <int WT, bool A32, int EPI, int NB>
+void launch_gemv_mf(const GemmDesc& d, hipStream_t s) {
+  const int per = (EPI == EPI_SWIGLU_F16 ? 8 : 16) * NB;
+  hipLaunchKernelGGL((k_gemv_mf<WT, A32, EPI, NB>), dim3((d.N + per - 1) / per), dim3(64 * MF_WAVES), 0, s, d);
+  check_hip(hipGetLastError(), "k_gemv_mf launch");
+}
+
+// Four column groups a workgroup once that still leaves a workgroup per CU (N >= 16384
+// columns; 8192 SwiGLU units), two from half that; one below.
 template <int WT, bool A32, int EPI>
 void run_gemv_mf(const GemmDesc& d, hipStream_t s) {
   if (d.row_ssq || d.norm_out) throw Error(T0H_ERR_HIP, "internal: split RMSNorm on a kernel without it");
-  const int per = EPI == EPI_SWIGLU_F16 ? 8 : 16;
-  hipLaunchKernelGGL((k_gemv_mf<WT, A32, EPI>), dim3((d.N + per - 1) / per), dim3(64 * MF_WAVES), 0, s, d);
-  check_hip(hipGetLastError(), "k_gemv_mf launch");
+  const int groups = (d.N + (EPI == EPI_SWIGLU_F16 ? 7 : 15)) / (EPI == EPI_SWIGLU_F16 ? 8 : 16);
+  if (groups >= 4 * 256) return launch_gemv_mf<WT, A32, EPI, 4>(d, s);
+  if (groups >= 2 * 256) return launch_gemv_mf<WT, A32, EPI, 2>(d, s);
+  launch_gemv_mf<WT, A32, EPI, 1>(d, s);
 }
 
 // The f32-MFMA small-M kernel's operand loads: 16-byte activation chunks and,
