@@ -220,10 +220,12 @@ def gemm_sweep(torch, t0hip, iters=20):
             for M in ((1, 16) if N * K > 2**24 else (1, 16, 64, 512, 8192)):
                 # rotate weight copies past the 256 MB Infinity Cache for the bandwidth-bound cases
                 n_copies = max(1, int(np.ceil(320e6 / blocks.size))) if M <= 64 else 1
-                dW = torch.from_numpy(blocks).cuda().repeat(n_copies)
+                # copies 256-byte aligned (the GEMM entry points take 16-byte aligned weights)
+                src = np.concatenate([blocks, np.zeros((-blocks.size) % 256, np.uint8)])
+                dW = torch.from_numpy(src).cuda().repeat(n_copies)
                 x = torch.randn((M, K), dtype=torch.float32, device="cuda")
                 y = torch.empty((M, N), dtype=torch.float32, device="cuda")
-                stride = blocks.size
+                stride = src.size
 
                 def run(i):
                     t0hip.gemm_q_dev(qtype, dW.data_ptr() + (i % n_copies) * stride, x.data_ptr(), 0, y.data_ptr(),

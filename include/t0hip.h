@@ -213,7 +213,9 @@ int t0h_forecast_grouped_ar(t0h_model* model, const float* contexts, const int64
 int t0h_forecast_rollout(t0h_model* model, const float* context, size_t t_ctx, size_t prediction_length,
                          const float* query_levels, size_t n_query, float* out, size_t out_len);
 
-/* ---- kernel-level entry points (device pointers, stream = hipStream_t or NULL) ---- */
+/* ---- kernel-level entry points (device pointers, stream = hipStream_t or NULL) ----
+ * The GEMM entry points take d_w, d_x and d_y 16-byte aligned (as hipMalloc returns
+ * them) and d_bias 4-byte aligned; other pointers are refused with T0H_ERR_INVALID_ARG. */
 /* Bit-exact dequantization ≡ dequantize_for (gguf.rs:213-226) on device. */
 int t0h_dequant(int qtype, const void* d_blocks, size_t n_elements, float* d_out, void* stream);
 /* ≡ t0-fast linear() (model.rs:406-504) / ops::linear (ops.rs:40-42):

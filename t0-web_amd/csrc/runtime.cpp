@@ -1657,10 +1657,18 @@ int t0h_dequant(int qtype, const void* d_blocks, size_t n, float* d_out, void* s
   API_END
 }
 
+// The kernel-level entry points' operands: the kernels move weights, activations and outputs in
+// 16-byte vectors, so the base pointers must be 16-byte aligned (as hipMalloc returns them).
+static bool gemm_ptrs_aligned(const void* w, const void* x, const void* y, const void* bias) {
+  auto a = [](const void* p, uintptr_t m) { return (reinterpret_cast<uintptr_t>(p) & (m - 1)) == 0; };
+  return a(w, 16) && a(x, 16) && a(y, 16) && a(bias, 4);
+}
+
 int t0h_gemm_q(int wtype, const void* d_w, const float* d_x, const float* d_bias, float* d_y, size_t m, size_t n,
                size_t k, int act, void* stream) {
   API_BEGIN
   require(m < (1u << 31) && n < (1u << 31) && k < (1u << 31), "t0h_gemm_q: dimension too large");
+  require(gemm_ptrs_aligned(d_w, d_x, d_y, d_bias), "t0h_gemm_q: d_w, d_x and d_y must be 16-byte aligned");
   GemmDesc d;
   d.wtype = wtype;
   d.w = d_w;
@@ -1685,6 +1693,7 @@ int t0h_gemm_f16(int wtype, const void* d_w, const void* d_x, const float* d_bia
   require(m < (1u << 31) && n < (1u << 31) && k < (1u << 31), "t0h_gemm_f16: dimension too large");
   require(epilogue >= EPI_STORE_F32 && epilogue <= EPI_SWIGLU_F16, "t0h_gemm_f16: unknown epilogue");
   require(tile >= 0 && tile <= 8 && tile != 2, "t0h_gemm_f16: tile must be 0, 1 or 3..8");
+  require(gemm_ptrs_aligned(d_w, d_x, d_y, d_bias), "t0h_gemm_f16: d_w, d_x and d_y must be 16-byte aligned");
   GemmDesc d;
   d.wtype = wtype;
   d.w = d_w;

@@ -68,6 +68,12 @@ def test_host_entry_points_validate(t0hip):
     x = np.zeros(64, np.float32)
     out = np.zeros(10, np.uint8)
     assert L.t0h_quantize(8, x.ctypes.data_as(C.c_void_p), 64, out.ctypes.data_as(C.c_void_p), 10) == -1
+    # the GEMM entry points refuse base pointers their 16-byte vector accesses cannot use
+    P = C.c_void_p
+    assert L.t0h_gemm_q(8, P(0x1008), P(0x2000), None, P(0x3000), 1, 64, 64, 0, None) == -1
+    assert L.t0h_gemm_q(8, P(0x1000), P(0x2000), P(0x4002), P(0x3000), 1, 64, 64, 0, None) == -1
+    assert L.t0h_gemm_f16(8, P(0x1000), P(0x2004), None, P(0x3000), 1, 64, 64, 0, 0, None) == -1
+    assert b"16-byte aligned" in L.t0h_last_error()
 
 
 def test_no_cpu_fallback_in_product():
