@@ -746,6 +746,118 @@ __global__ __launch_bounds__(256) void k_group_attn_seg(const AttnDesc d) {
   *reinterpret_cast<uint4*>(d.out + m * E + h * HD + d0) = __builtin_bit_cast(uint4, hv);
 }
 
+// Group attention by segment: one 8-lane group per (segment, patch, head), each
+// lane owning 8 of the 64 dims.  The group loads the q, k and v chunks of every
+// member of the segment once and computes every member's query, where
+// k_group_attn_seg loads every member's k and v once per query.  The arithmetic of
+// a (query, key) pair, and its order, is k_group_attn_seg's, so the results are
+// the same.  Three memory round trips a task: the segment's bounds, its
+// permutation entries, the members' group ids and chunks (members past the
+// segment read its last row and are excluded).
+template <int MAXG>
+__global__ __launch_bounds__(256) void k_group_attn_sw(const AttnDesc d) {
+  const int H = d.heads, E = d.E, p = d.p, v = d.v, ld = 3 * E;
+  const long long task = ((long long)blockIdx.x * 256 + threadIdx.x) >> 3;
+  const int sub = threadIdx.x & 7, d0 = sub * 8;
+  if (task >= (long long)d.n_seg * p * H) return;  // whole 8-lane groups exit together
+  const int h = (int)(task % H);
+  const long long sp = task / H;
+  const int sg = (int)(sp / p), pi = (int)(sp % p);
+  const _Float16* col = d.qkv + (size_t)h * HD + d0;
+  const int b = d.seg_start[sg];
+  const int n = (sg + 1 < d.n_seg ? d.seg_start[sg + 1] : v) - b;  // >= 1
+  float qs[8], kn[8];
+  load_f8(d.q_norm + d0, qs);
+  load_f8(d.k_norm + d0, kn);
+  int jr[MAXG];
+#pragma unroll
+  for (int i = 0; i < MAXG; ++i) jr[i] = d.perm[b + min(i, n - 1)];
+  int g[MAXG];
+  uint4 qr[MAXG], kr[MAXG], vr[MAXG];
+#pragma unroll
+  for (int i = 0; i < MAXG; ++i) {
+    const long long mk = (long long)jr[i] * p + pi;
+    g[i] = d.grp[mk];
+    qr[i] = *reinterpret_cast<const uint4*>(col + mk * ld);
+    kr[i] = *reinterpret_cast<const uint4*>(col + mk * ld + E);
+    vr[i] = *reinterpret_cast<const uint4*>(col + mk * ld + 2 * E);
+  }
+  __builtin_amdgcn_sched_barrier(0);  // every member's loads issued before the first is used
+  // per member key: k * k_norm and its RMS, once for all queries
+  float kk[MAXG][8], krs[MAXG];
+#pragma unroll
+  for (int i = 0; i < MAXG; ++i) {
+    float kx[8];
+    unpack8(kr[i], kx);
+    float ks = 0.0f;
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+      ks += kx[e] * kx[e];
+      kk[i][e] = kx[e] * kn[e];
+    }
+    krs[i] = sqrtf(lane_sum8(ks) / (float)HD + 1e-8f);
+  }
+#pragma unroll
+  for (int a = 0; a < MAXG; ++a) {
+    if (a >= n) break;
+    const int gq = g[a];
+    float o[8];
+#pragma unroll
+    for (int e = 0; e < 8; ++e) o[e] = 0.0f;
+    {
+      float qn[8];
+      unpack8(qr[a], qn);
+      float ss = 0.0f;
+#pragma unroll
+      for (int e = 0; e < 8; ++e) ss += qn[e] * qn[e];
+      const float dq = sqrtf(lane_sum8(ss) / (float)HD + 1e-8f);
+#pragma unroll
+      for (int e = 0; e < 8; ++e) qn[e] = (qn[e] / dq) * qs[e];
+      float sc[MAXG];
+      float mx = -INFINITY;
+#pragma unroll
+      for (int i = 0; i < MAXG; ++i) {
+        float dot = 0.0f;
+#pragma unroll
+        for (int e = 0; e < 8; ++e) dot += qn[e] * kk[i][e];
+        dot = lane_sum8(dot);
+        sc[i] = i < n && g[i] == gq ? (dot / krs[i]) * 0.125f : -INFINITY;
+        mx = fmaxf(mx, sc[i]);
+      }
+      float l = 0.0f;
+#pragma unroll
+      for (int i = 0; i < MAXG; ++i) {
+        const float pw = i < n && g[i] == gq ? __expf(sc[i] - mx) : 0.0f;
+        float vx[8];
+        unpack8(vr[i], vx);
+        l += pw;
+#pragma unroll
+        for (int e = 0; e < 8; ++e) o[e] += pw * vx[e];
+      }
+      const float inv = 1.0f / l;  // the query's own row is in its segment with its group: l >= 1
+#pragma unroll
+      for (int e = 0; e < 8; ++e) o[e] *= inv;
+    }
+    if (gq < 0) {  // all-PAD patch: every score is -1e9, uniform weights over all v rows
+#pragma unroll
+      for (int e = 0; e < 8; ++e) o[e] = 0.0f;
+      for (int j = 0; j < v; ++j) {
+        float vv[8];
+        unpack8(*reinterpret_cast<const uint4*>(col + ((long long)j * p + pi) * ld + 2 * E), vv);
+#pragma unroll
+        for (int e = 0; e < 8; ++e) o[e] += vv[e];
+      }
+      const float inv = 1.0f / (float)v;
+#pragma unroll
+      for (int e = 0; e < 8; ++e) o[e] *= inv;
+    }
+    half8 hv;
+#pragma unroll
+    for (int e = 0; e < 8; ++e) hv[e] = (_Float16)o[e];
+    *reinterpret_cast<uint4*>(d.out + ((long long)jr[a] * p + pi) * E + h * HD + d0) = __builtin_bit_cast(uint4, hv);
+  }
+}
+
 void check_hip(hipError_t e, const char* what) {
   if (e != hipSuccess) throw Error(T0H_ERR_HIP, std::string(what) + ": " + hipGetErrorString(e));
 }
@@ -817,7 +929,19 @@ void launch_group_attention(const AttnDesc& d, hipStream_t s) {
   if (!d.perm || !d.seg_begin || !d.seg_len) throw Error(T0H_ERR_INVALID_ARG, "group attention: null segment arrays");
   const long long lanes = (long long)d.v * d.p * d.heads * 8;
   const dim3 grid((unsigned)((lanes + 255) / 256));
-  if (d.seg_max <= 4)
+  // by segment when the segment list is there (one task a segment, patch and head)
+  const long long seg_lanes = (long long)d.n_seg * d.p * d.heads * 8;
+  const dim3 seg_grid((unsigned)((seg_lanes + 255) / 256));
+  const bool by_seg = d.seg_start && d.n_seg > 0;
+  if (d.seg_max <= 2 && by_seg)
+    hipLaunchKernelGGL(k_group_attn_sw<2>, seg_grid, dim3(256), 0, s, d);
+  else if (d.seg_max == 3 && by_seg)
+    hipLaunchKernelGGL(k_group_attn_sw<3>, seg_grid, dim3(256), 0, s, d);
+  else if (d.seg_max <= 4 && by_seg)
+    hipLaunchKernelGGL(k_group_attn_sw<4>, seg_grid, dim3(256), 0, s, d);
+  else if (d.seg_max <= 8 && by_seg)
+    hipLaunchKernelGGL(k_group_attn_sw<8>, seg_grid, dim3(256), 0, s, d);
+  else if (d.seg_max <= 4)
     hipLaunchKernelGGL(k_group_attn_seg<4>, grid, dim3(256), 0, s, d);
   else if (d.seg_max <= 8)
     hipLaunchKernelGGL(k_group_attn_seg<8>, grid, dim3(256), 0, s, d);

@@ -107,6 +107,8 @@ struct AttnDesc {
   const int* seg_begin = nullptr;    // [v]
   const int* seg_len = nullptr;      // [v]
   int seg_max = 0;                   // longest segment (selects the kernel)
+  const int* seg_start = nullptr;    // [n_seg] first permutation index of each segment
+  int n_seg = 0;
   int qsplit = 1;                    // time attention: workgroups per (row, head), set by the launcher
   // time attention past T0H_LDS_PATCHES patches: workspace for the prepared keys
   // [v][heads][P32][64], the transposed values [v][heads][64][P32] and the key

@@ -71,17 +71,18 @@ struct Stage {
 
 // A window forward captured as a HIP graph.  It is replayed only while every
 // value the captured launches bake in is unchanged: the window shape, the
-// longest group segment (which picks the group-attention kernel), the input
+// longest group segment (which picks the group-attention kernel) and the
+// segment count (its grid), the input
 // and output pointers and the workspace generation (the allocation count, so
 // that a buffer reallocated since the capture is never replayed).
 struct GraphKey {
-  int v = 0, t_ctx = 0, horizon = 0, seg_max = 0;
+  int v = 0, t_ctx = 0, horizon = 0, seg_max = 0, n_seg = 0;
   const void* ctx = nullptr;
   const void* out = nullptr;
   uint64_t ws_gen = 0;
   bool operator==(const GraphKey& o) const {
-    return v == o.v && t_ctx == o.t_ctx && horizon == o.horizon && seg_max == o.seg_max && ctx == o.ctx &&
-           out == o.out && ws_gen == o.ws_gen;
+    return v == o.v && t_ctx == o.t_ctx && horizon == o.horizon && seg_max == o.seg_max && n_seg == o.n_seg &&
+           ctx == o.ctx && out == o.out && ws_gen == o.ws_gen;
   }
 };
 struct GraphEntry {
@@ -98,6 +99,7 @@ struct Workspace {
   uint64_t allocs = 0;
   int rope_p = -1;
   int seg_max = 0;  // longest group segment of the last upload_segments
+  int n_seg = 0;    // and its number of segments
   bool capturing = false;  // a graph capture is recording this model's launches
   bool graphs = true;      // window forwards are captured and replayed
   std::vector<GraphEntry> graph_cache;
@@ -503,7 +505,7 @@ void rope_tables(int p, int hd, std::vector<float>& cs, std::vector<float>& sn, 
 // ---- group segments: rows sorted by group; per row its segment -------------
 void upload_segments(t0h_model* m, const std::vector<int64_t>& row_group, bool consistent) {
   const int v = (int)row_group.size();
-  std::vector<int> perm(v), begin(v), len(v);
+  std::vector<int> perm(v), begin(v), len(v), starts;
   std::iota(perm.begin(), perm.end(), 0);
   if (consistent) {
     std::stable_sort(perm.begin(), perm.end(), [&](int a, int b) { return row_group[a] < row_group[b]; });
@@ -515,16 +517,21 @@ void upload_segments(t0h_model* m, const std::vector<int64_t>& row_group, bool c
         begin[perm[k]] = i;
         len[perm[k]] = j - i;
       }
+      starts.push_back(i);
       i = j;
     }
   } else {  // arbitrary per-patch groups: every row scans all rows (group equality is checked per key)
     std::fill(begin.begin(), begin.end(), 0);
     std::fill(len.begin(), len.end(), v);
+    if (v) starts.push_back(0);
   }
   put_cached(m, "perm", perm.data(), v);
   put_cached(m, "seg_begin", begin.data(), v);
   put_cached(m, "seg_len", len.data(), v);
+  ws_get<int>(m, "seg_start", v);  // sized for the most segments, so the count may vary without a regrow
+  if (!starts.empty()) put_cached(m, "seg_start", starts.data(), starts.size());
   m->ws.seg_max = v ? *std::max_element(len.begin(), len.end()) : 0;
+  m->ws.n_seg = (int)starts.size();
 }
 
 // Per layer and side (q, k), one [p, 128] f32 table folding the QK-norm scale,
@@ -621,6 +628,7 @@ void encode_and_layers(t0h_model* m, int v, int p, const PatchMeta& pm, float* t
   const int* perm = ws_get<int>(m, "perm", v);
   const int* seg_begin = ws_get<int>(m, "seg_begin", v);
   const int* seg_len = ws_get<int>(m, "seg_len", v);
+  const int* seg_start = ws_get<int>(m, "seg_start", v);
   if (!m->ws.arena.on && m->ws.rope_p != p) throw Error(T0H_ERR_HIP, "internal: RoPE tables not prepared for this window");
 
   // RMSNorm split across the GEMMs either side of it (ops.rs:12-17): each residual
@@ -698,6 +706,8 @@ void encode_and_layers(t0h_model* m, int v, int p, const PatchMeta& pm, float* t
   ad.seg_begin = seg_begin;
   ad.seg_len = seg_len;
   ad.seg_max = m->ws.seg_max;
+  ad.seg_start = seg_start;
+  ad.n_seg = m->ws.n_seg;
   if (p > T0H_LDS_PATCHES) {  // the long-window time attention's key workspace
     const size_t P32 = (size_t)(p + 31) / 32 * 32;
     ad.kr = ws_get<_Float16>(m, "attn_kr", (size_t)v * P32 * E);
@@ -903,7 +913,7 @@ void forecast_window(t0h_model* m, const WindowRows& wr, float* d_out) {
   const PatchMeta pm = patch_buffers(m, v, p);
   reserve_forward(m, v, p, v * std::max(hp, 1));
   ws_get<int64_t>(m, "win_off", v);
-  for (const char* n : {"win_len", "win_grp", "perm", "seg_begin", "seg_len"}) ws_get<int>(m, n, v);
+  for (const char* n : {"win_len", "win_grp", "perm", "seg_begin", "seg_len", "seg_start"}) ws_get<int>(m, n, v);
   ws_get<float>(m, "rope", m->layers.size() * 2 * (size_t)p * 128);
   uint8_t* prep_rows = prep_fits_lds(t, ps) ? nullptr : ws_get<uint8_t>(m, "prep_rows", (size_t)v * prep_row_bytes(t, ps));
 
@@ -960,6 +970,7 @@ void forecast_window(t0h_model* m, const WindowRows& wr, float* d_out) {
   key.t_ctx = wr.t_ctx;
   key.horizon = wr.horizon;
   key.seg_max = m->ws.seg_max;
+  key.n_seg = m->ws.n_seg;
   key.ctx = wr.d_ctx;
   key.out = d_out;
   key.ws_gen = m->ws.allocs;
