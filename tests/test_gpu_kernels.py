@@ -271,9 +271,24 @@ def test_small_m_f32_mfma_kernel(torch_cuda, t0hip, oracle, rng, qtype, m, k, n)
 
 
 @pytest.mark.parametrize("qtype", [8, 2, 1])
+@pytest.mark.parametrize("m,k,n", [(16, 256, 16400), (5, 512, 8200), (2, 96, 16384)])
+def test_small_m_wide_matrix(torch_cuda, t0hip, oracle, rng, qtype, m, k, n):
+    """The f32-MFMA small-M kernel with two (N >= 8192) and four (N >= 16384) groups of 16 columns
+    a workgroup: exact f32 products, the 1e-5 gate, with and without ReLU; N ragged against 64."""
+    W = (0.02 * rng.standard_normal((n, k))).astype(np.float32)
+    x = rng.standard_normal((m, k)).astype(np.float32)
+    b = (0.02 * rng.standard_normal(n)).astype(np.float32)
+    blocks = oracle.quantize(qtype, W)
+    deq = oracle.dequantize(qtype, blocks, n * k).reshape(n, k).astype(np.float64)
+    want = x.astype(np.float64) @ deq.T + b
+    assert rel_err(run_gemm(torch_cuda, t0hip, qtype, blocks, x, b, n), want) < 1e-5, (m, k, n)
+    assert rel_err(run_gemm(torch_cuda, t0hip, qtype, blocks, x, b, n, act=1), np.maximum(want, 0.0)) < 1e-5
+
+
+@pytest.mark.parametrize("qtype", [8, 2, 1])
 @pytest.mark.parametrize("epi", [0, 1, 2, 3])
 @pytest.mark.parametrize("m,k,n", [(1, 768, 136), (1, 4096, 136), (1, 8192, 40), (9, 2048, 72), (16, 768, 40),
-                                   (2, 96, 24)])
+                                   (2, 96, 24), (7, 256, 8200), (16, 256, 16400)])
 def test_small_m_forward_epilogues(torch_cuda, t0hip, oracle, rng, qtype, epi, m, k, n):
     """The forward's GEMMs at M <= 16 (a single series, the decoder's forecast rows): f16
     activations, epilogues bias / f16 store / residual add / SwiGLU on the small-M kernels
