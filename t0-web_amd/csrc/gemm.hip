@@ -45,6 +45,9 @@ typedef _Float16 half2v __attribute__((ext_vector_type(2)));
 typedef float floatx4 __attribute__((ext_vector_type(4)));
 typedef float floatx16 __attribute__((ext_vector_type(16)));
 typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+// Four dwords at a 4-byte-aligned address (a Q8_0 / Q4_0 span): still one 16-byte load on gfx950,
+// without the 16-byte alignment a uint4 access would promise the compiler.
+typedef uint32_t u32x4_a4 __attribute__((ext_vector_type(4), aligned(4)));
 
 constexpr int TK = 64, LDK = TK + 8;
 
@@ -1715,7 +1718,7 @@ __global__ __launch_bounds__(256) void k_gemv_s(const GemmDesc d) {
     const uint32_t* src = wr + min(t * 16 + sp, nsp - 1) * DW;
 #pragma unroll
     for (int q = 0; q < DW / 4; ++q) {
-      const uint4 u = *reinterpret_cast<const uint4*>(src + 4 * q);
+      const u32x4_a4 u = *reinterpret_cast<const u32x4_a4*>(src + 4 * q);
       w[t][4 * q] = u.x, w[t][4 * q + 1] = u.y, w[t][4 * q + 2] = u.z, w[t][4 * q + 3] = u.w;
     }
     w[t][DW - 1] = src[DW - 1];
@@ -1874,7 +1877,7 @@ __global__ __launch_bounds__(256) void k_gemv_w(const GemmDesc d) {
       const uint32_t* src = wr + (lane + 64 * j) * DW;
 #pragma unroll
       for (int q = 0; q < DW / 4; ++q) {
-        const uint4 u = *reinterpret_cast<const uint4*>(src + 4 * q);
+        const u32x4_a4 u = *reinterpret_cast<const u32x4_a4*>(src + 4 * q);
         w[i][j][4 * q] = u.x, w[i][j][4 * q + 1] = u.y, w[i][j][4 * q + 2] = u.z, w[i][j][4 * q + 3] = u.w;
       }
       w[i][j][DW - 1] = src[DW - 1];
