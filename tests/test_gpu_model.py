@@ -240,6 +240,22 @@ def test_grouped_multivariate(models, t0hip, oracle, engine, rng):
     assert_close(got, want, scale=row_scale(ctx))
 
 
+@pytest.mark.parametrize("sizes", [(1, 3, 5, 8, 2), (4, 1, 4, 3), (2, 2, 1)])
+def test_grouped_ragged_segments(models, t0hip, oracle, engine, rng, sizes):
+    """Groups of different sizes in one batch, their rows interleaved in the input order: the group
+    attention's segments (largest 8, 4 and 2 rows) hold fewer members than the kernel instance, and
+    a segment's rows are not adjacent rows of the batch."""
+    gm, om = models[("small", 2)]
+    t_ctx, h = 512, 32
+    groups = np.concatenate([np.full(n, 11 * g + 5, np.int64) for g, n in enumerate(sizes)])
+    groups = groups[rng.permutation(len(groups))]
+    v = len(groups)
+    ctx = nan_gaps(rng, sine_mix(rng, v, t_ctx) * np.exp(rng.standard_normal(v)).astype(np.float32)[:, None])
+    got = t0hip.forecast_grouped(engine, gm, ctx, groups, t_ctx, h)
+    want = om.forecast_grouped(ctx, groups, t_ctx, h)
+    assert_close(got, want, scale=row_scale(ctx))
+
+
 def test_grouped_ar(models, t0hip, oracle, engine, rng):
     """BASELINE config 5 shape (scaled down): AR steps append each row's median quantile.
     (1) The GPU loop equals the GPU's single-step forecasts on the windows it builds (the device
