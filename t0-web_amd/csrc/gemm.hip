@@ -1056,6 +1056,17 @@ __global__ __launch_bounds__(64 * NWV) __attribute__((amdgpu_waves_per_eu(2, 2))
   const int total = gridDim.x, bid = blockIdx.x, per = total / 8;
   const int t = bid < per * 8 ? (bid % 8) * per + bid / 8 : bid;
   const int tn = t % tiles_n, m0 = (t / tiles_n) * BM;
+  // Two workgroups share a CU here, and with equal tiles they would start, reach
+  // their epilogues and store together for the whole launch.  The second one of
+  // each CU in the first round (blocks 256 .. 511 on the 256 CUs) starts about
+  // 7 us late, so that one's epilogue stores overlap the other's MFMAs (config-4
+  // step 0.7-0.8 % shorter, A/B on two boxes; 3.4 or 10 us measured less).
+  if constexpr (NWV == 4) {
+    if (total > 512 && bid >= 256 && bid < 512) {
+      __builtin_amdgcn_s_sleep(127);  // 127 x 64 cycles
+      __builtin_amdgcn_s_sleep(127);
+    }
+  }
 
   // Activation chunk t%8 of rows t/8 + AQS q (rows past M read row M-1,
   // never stored) as byte offsets from the tile's first row; the lane's weight
